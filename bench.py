@@ -1,0 +1,238 @@
+"""Benchmark of the FA3 backward (shaobo_fa3_bwd_v2) on one MI355X.
+
+A step is one full backward lifecycle (delta preprocess -> main kernel -> dQ
+finalize) through the C ABI over resident fp16 inputs at the headline shape
+B=1, H=4, S=2048, D=128, causal.  Prints one JSON
+line: TFLOP/s from FLOPs = 10*B*H*S^2*D*0.5, ms per backward, % of fp16 dense
+MFMA peak, the main kernel's roofline (HIP events recorded by the library at
+its stage boundaries on the null stream, where it launches), and the CPU
+oracle timed on the host as the reported CPU baseline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config P3]
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "flash-attention3_amd"))
+
+METRIC = "FA bwd TFLOPS + % fp16 MFMA peak, B1 H4 S2048 D128 causal fp16; ms/bwd"
+FP16_PEAK_TFLOPS = 2516.6   # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
+HBM_PEAK_GBS = 8000.0
+STAGE_TAG = 0x53544745      # reserved_i32[15]: record stage events (library hook)
+
+CONFIGS = {
+    # name: (B, Hq, Hkv, S, D, causal)
+    "P1": (1, 1, 1, 128, 128, True),
+    "P2": (1, 1, 1, 1024, 128, True),
+    "P3": (1, 4, 4, 2048, 128, True),
+    "P4": (2, 32, 8, 4096, 128, True),
+    "P5": (2, 16, 16, 8192, 64, False),
+}
+
+
+def flops(B, Hq, S, D, causal):
+    return 10.0 * B * Hq * S * S * D * (0.5 if causal else 1.0)
+
+
+def make_inputs(torch, B, Hq, Hkv, S, D, causal, scale, seed=1234):
+    """Seeded N(0,1) fp16 Q, K, V, dO; O and natural LSE from an fp32 GPU
+    forward (input preparation, outside the timed region)."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    mk = lambda h: torch.randn((B, h, S, D), generator=gen, device="cuda").half()  # noqa: E731
+    q, k, v, do = mk(Hq), mk(Hkv), mk(Hkv), mk(Hq)
+    out = torch.empty_like(q)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device="cuda")
+    G = Hq // Hkv
+    mask = torch.triu(torch.ones(S, S, dtype=torch.bool, device="cuda"), 1) if causal else None
+    for b in range(B):
+        for h in range(Hq):
+            s = torch.mm(q[b, h].float(), k[b, h // G].float().t().contiguous()) * scale
+            if mask is not None:
+                s.masked_fill_(mask, float("-inf"))
+            lse[b, h] = torch.logsumexp(s, -1)
+            out[b, h] = torch.mm(torch.softmax(s, -1), v[b, h // G].float()).half()
+            del s
+    return q, k, v, do, out, lse
+
+
+class Hip:
+    """Minimal hipEvent binding (events on the null stream)."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.lib.hipDeviceSynchronize.argtypes = []
+
+    def event(self):
+        e = ctypes.c_void_p()
+        assert self.lib.hipEventCreate(ctypes.byref(e)) == 0
+        return e
+
+    def record(self, e):
+        assert self.lib.hipEventRecord(e, None) == 0
+
+    def elapsed_ms(self, a, b):
+        self.lib.hipEventSynchronize(b)
+        ms = ctypes.c_float()
+        assert self.lib.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+    def sync(self):
+        assert self.lib.hipDeviceSynchronize() == 0
+
+
+def cpu_baseline(cfg, budget_s):
+    """Time the CPU oracle's backward (fp32, threaded) on a bounded sample of
+    the same workload: whole (batch, kv-head) groups of the config, repeated
+    until about budget_s seconds of CPU work have run."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import fa3_oracle as O
+    B, Hq, Hkv, S, D, causal = cfg
+    scale = 1.0 / math.sqrt(D)
+    threads = O.default_threads()
+    # whole config when small (P1-P3), else one (batch, kv-head) group
+    groups = B * Hkv if B * Hq * S <= 8192 else 1
+    x = O.make_inputs(B, Hq, Hkv, S, D)
+    out, smax, ssum, _ = O.forward(x["q"], x["k"], x["v"], causal, scale, (0, groups), threads)
+    runs, t_total = 0, 0.0
+    while t_total < budget_s or runs == 0:
+        t0 = time.perf_counter()
+        O.backward(x["q"], x["k"], x["v"], out, x["dout"], smax, ssum, causal, scale, (0, groups),
+                   threads)
+        t_total += time.perf_counter() - t0
+        runs += 1
+        if runs >= 1000:
+            break
+    sample_heads = groups * (Hq // Hkv)
+    f = flops(1, sample_heads, S, D, causal)
+    sec = t_total / runs
+    return {"value": round(f / sec / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle fp32 backward of {sample_heads} of {B * Hq} query heads "
+                      f"(S={S}, D={D}, causal={causal}), {runs} runs, {sec * 1e3:.1f} ms each",
+            "ms_per_bwd_sample": round(sec * 1e3, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="P3", choices=sorted(CONFIGS))
+    ap.add_argument("--deterministic", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0,
+                    help="seconds of CPU oracle work for cpu_baseline (0 disables)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested); the backward shards by (batch, kv-head) "
+              f"with no communication, so per-GPU throughput is the N=1 figure.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import shaobo_fa3 as F
+
+    B, Hq, Hkv, S, D, causal = CONFIGS[args.config]
+    scale = 1.0 / math.sqrt(D)
+    lib = F.load()
+    hip = Hip()
+    q, k, v, do, out, lse = make_inputs(torch, B, Hq, Hkv, S, D, causal, scale)
+    p = F.make_params(lib, batch=B, seqlen=S, heads_q=Hq, heads_kv=Hkv, head_dim=D,
+                      causal=causal, softmax_scale=scale, deterministic=args.deterministic)
+    nbytes = lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    delta = torch.empty((B, Hq, S), dtype=torch.float32, device="cuda")
+    c = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    argv = [c(do), c(q), c(k), c(v), c(out), c(lse), c(dq), c(dk), c(dv), c(delta)]
+
+    def step():
+        st = lib.shaobo_fa3_bwd_v2(*argv, ctypes.byref(p))
+        if st != F.SUCCESS:
+            raise RuntimeError("shaobo_fa3_bwd_v2: " + F.status_name(st))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # ---- timed region: exactly `steps` backward lifecycles ----
+    e0, e1 = hip.event(), hip.event()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    hip.record(e0)
+    for _ in range(args.steps):
+        step()
+    hip.record(e1)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = hip.elapsed_ms(e0, e1) / args.steps
+    f = flops(B, Hq, S, D, causal)
+    tflops = f / (ms * 1e-3) / 1e12
+
+    # ---- per-stage durations from the library's stage events ----
+    evs = [hip.event() for _ in range(4)]
+    p.reserved_i32[15] = STAGE_TAG
+    for i, e in enumerate(evs):
+        p.reserved_ptr[4 + i] = e.value
+    stage = [0.0, 0.0, 0.0]
+    for _ in range(args.steps):
+        step()
+        hip.sync()
+        for i in range(3):
+            stage[i] += hip.elapsed_ms(evs[i], evs[i + 1])
+    p.reserved_i32[15] = 0
+    stage = [s / args.steps for s in stage]
+    main_ms = stage[1]
+    rows = B * Hq * S
+    pre_bytes = rows * D * 2 * 2 + rows * 4 * 3 + rows * D * 4  # O, dO, LSE in; delta, lse2 out; dQ acc clear
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": f"fa3_bwd_v2 {args.config} B{B} Hq{Hq} Hkv{Hkv} S{S} D{D} "
+                               f"{'causal' if causal else 'full'}",
+                   "batch": B, "heads_q": Hq, "heads_kv": Hkv, "seq_len": S, "head_dim": D,
+                   "causal": causal, "deterministic": args.deterministic,
+                   "flops_per_bwd": f},
+        "pct_fp16_peak": round(100.0 * tflops / FP16_PEAK_TFLOPS, 3),
+        "wall_s_timed": round(wall, 4),
+        "stages_ms": {"preprocess": round(stage[0], 5), "main": round(stage[1], 5),
+                      "dq_finalize": round(stage[2], 5)},
+        "roofline": {"kernel": "bwd_main_kernel", "bound": "mfma",
+                     "achieved": round(f / (main_ms * 1e-3) / 1e12, 3),
+                     "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(f / (main_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 5),
+                     "traffic": None},
+        "preprocess_roofline": {"bound": "hbm",
+                                "achieved": round(pre_bytes / (stage[0] * 1e-3) / 1e9, 1),
+                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(pre_bytes / (stage[0] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+    }
+    if args.cpu_budget > 0:
+        result["cpu_baseline"] = cpu_baseline(CONFIGS[args.config], args.cpu_budget)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,281 @@
+// C ABI of libshaobo_fa3_bwd.so: parameter validation, capability report,
+// workspace sizing and the v2 / legacy / component entry points.
+//
+// Behavioural contract (reference src/shaobo_fa3_bwd_api.cpp):
+//   * validate before any dispatch; INVALID_VALUE for malformed input,
+//     UNSUPPORTED for well-formed requests outside the capability set
+//     (:70-120), null tensors / short workspace -> INVALID_VALUE (:221-231);
+//   * default scale 1/sqrt(head_dim_qk) when softmax_scale_is_set == 0
+//     (:241-243); softmax_d optional (:234-236);
+//   * all work on the null stream, asynchronous unless sync_after_launch
+//     (:254-259); HIP launch failures -> HIP_ERROR.
+// Extension over the reference: head_dim 64 is accepted besides 128.
+#include "shaobo_fa3_api.h"
+#include "shaobo_fa3_components.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstddef>
+#include <cstring>
+#include <limits>
+
+#include "fa3_bwd_internal.h"
+
+// The struct layout is part of the ABI: pin it (reference header order,
+// x86-64 SysV offsets).
+static_assert(offsetof(ShaoboFa3Params, struct_size) == 0, "abi");
+static_assert(offsetof(ShaoboFa3Params, batch) == 4, "abi");
+static_assert(offsetof(ShaoboFa3Params, causal) == 32, "abi");
+static_assert(offsetof(ShaoboFa3Params, softmax_scale) == 44, "abi");
+static_assert(offsetof(ShaoboFa3Params, dtype) == 52, "abi");
+static_assert(offsetof(ShaoboFa3Params, sync_after_launch) == 76, "abi");
+static_assert(offsetof(ShaoboFa3Params, cu_seqlens_q) == 80, "abi");
+static_assert(offsetof(ShaoboFa3Params, cu_seqlens_k) == 88, "abi");
+static_assert(offsetof(ShaoboFa3Params, max_seqlen_q) == 96, "abi");
+static_assert(offsetof(ShaoboFa3Params, workspace) == 104, "abi");
+static_assert(offsetof(ShaoboFa3Params, workspace_bytes) == 112, "abi");
+static_assert(offsetof(ShaoboFa3Params, reserved_i32) == 120, "abi");
+static_assert(offsetof(ShaoboFa3Params, reserved_ptr) == 184, "abi");
+static_assert(offsetof(ShaoboFa3Params, seqused_q) == 248, "abi");
+static_assert(offsetof(ShaoboFa3Params, total_q) == 264, "abi");
+static_assert(offsetof(ShaoboFa3Params, softcap) == 280, "abi");
+static_assert(offsetof(ShaoboFa3Params, deterministic) == 284, "abi");
+static_assert(offsetof(ShaoboFa3Params, sm_margin) == 288, "abi");
+static_assert(offsetof(ShaoboFa3Params, softmax_scale_is_set) == 292, "abi");
+static_assert(sizeof(ShaoboFa3Params) == 296, "abi");
+static_assert(sizeof(ShaoboFa3BwdCapabilities) == 32, "abi");
+
+namespace {
+
+constexpr int kSequenceAlignment = 128;
+constexpr int kMinHeadDim = 64;
+constexpr int kMaxHeadDim = 128;
+
+bool is_flag(int32_t v) { return v == 0 || v == 1; }
+
+// Causal forces window_right = 0; windows at least as long as the sequence
+// are the same as unbounded (reference :53-68).
+bool window_is_full(const ShaoboFa3Params* p) {
+    int left = p->window_left >= p->seqlen_k - 1 ? -1 : p->window_left;
+    int right = p->window_right >= p->seqlen_q - 1 ? -1 : p->window_right;
+    if (p->causal) right = 0;
+    return left < 0 && (p->causal ? right == 0 : right < 0);
+}
+
+bool head_dim_supported(int d) { return d == 64 || d == 128; }
+
+int validate(const ShaoboFa3Params* p) {
+    if (p == nullptr || p->struct_size < sizeof(ShaoboFa3Params)) {
+        return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    }
+    const bool dims_ok = p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0 &&
+                         p->num_heads_q > 0 && p->num_heads_kv > 0 &&
+                         p->num_heads_q % p->num_heads_kv == 0;
+    const bool flags_ok = is_flag(p->causal) && is_flag(p->deterministic) &&
+                          is_flag(p->sync_after_launch) && is_flag(p->softmax_scale_is_set);
+    const bool scale_ok = p->softmax_scale_is_set == 0 ||
+                          (std::isfinite(p->softmax_scale) && p->softmax_scale >= 0.0f);
+    const bool softcap_ok = std::isfinite(p->softcap) && p->softcap >= 0.0f;
+    const bool dropout_ok = std::isfinite(p->dropout_p) && p->dropout_p >= 0.0f &&
+                            p->dropout_p < 1.0f;
+    if (!dims_ok || !flags_ok || !scale_ok || !softcap_ok || !dropout_ok) {
+        return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    }
+
+    const int64_t total_q = (int64_t)p->batch * p->seqlen_q;
+    const int64_t total_k = (int64_t)p->batch * p->seqlen_k;
+    const bool fixed_length =
+        p->cu_seqlens_q == nullptr && p->cu_seqlens_k == nullptr && p->seqused_q == nullptr &&
+        p->seqused_k == nullptr && (p->max_seqlen_q == 0 || p->max_seqlen_q == p->seqlen_q) &&
+        (p->max_seqlen_k == 0 || p->max_seqlen_k == p->seqlen_k) &&
+        (p->total_q == 0 || p->total_q == total_q) && (p->total_k == 0 || p->total_k == total_k);
+    if (!fixed_length || p->dtype != SHAOBO_FA3_DTYPE_FP16 ||
+        p->layout != SHAOBO_FA3_LAYOUT_BHSD || !head_dim_supported(p->head_dim_qk) ||
+        p->head_dim_v != p->head_dim_qk || p->seqlen_q != p->seqlen_k ||
+        p->seqlen_q % kSequenceAlignment != 0 || p->dropout_p != 0.0f || p->softcap != 0.0f ||
+        p->sm_margin != 0 || !window_is_full(p)) {
+        return SHAOBO_FA3_STATUS_UNSUPPORTED;
+    }
+    return SHAOBO_FA3_STATUS_SUCCESS;
+}
+
+fa3::BwdProblem problem_of(const ShaoboFa3Params* p) {
+    fa3::BwdProblem pr;
+    pr.batch = p->batch;
+    pr.seqlen = p->seqlen_q;
+    pr.heads_q = p->num_heads_q;
+    pr.heads_kv = p->num_heads_kv;
+    pr.head_dim = p->head_dim_qk;
+    pr.causal = p->causal != 0;
+    pr.deterministic = p->deterministic != 0;
+    pr.scale = p->softmax_scale_is_set ? p->softmax_scale
+                                       : 1.0f / std::sqrt((float)p->head_dim_qk);
+    return pr;
+}
+
+int finish(hipError_t err, const ShaoboFa3Params* p) {
+    if (err != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
+    if (p->sync_after_launch && hipDeviceSynchronize() != hipSuccess) {
+        return SHAOBO_FA3_STATUS_HIP_ERROR;
+    }
+    return SHAOBO_FA3_STATUS_SUCCESS;
+}
+
+// Shared body of v2 and the legacy entry.
+int run_backward(const void* dout, const void* q, const void* k, const void* v, const void* out,
+                 const void* aux0, const void* aux1, bool aux_is_lse, void* dq, void* dk,
+                 void* dv, void* softmax_d, const ShaoboFa3Params* params) {
+    const int status = validate(params);
+    if (status != SHAOBO_FA3_STATUS_SUCCESS) return status;
+    if (dout == nullptr || q == nullptr || k == nullptr || v == nullptr || out == nullptr ||
+        aux0 == nullptr || (!aux_is_lse && aux1 == nullptr) || dq == nullptr || dk == nullptr ||
+        dv == nullptr) {
+        return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    }
+    const fa3::BwdProblem pr = problem_of(params);
+    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr);
+    if (!plan.ok || params->workspace == nullptr || params->workspace_bytes < plan.total) {
+        return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    }
+    fa3::BwdTensors t;
+    t.dout = dout;
+    t.q = q;
+    t.k = k;
+    t.v = v;
+    t.out = out;
+    t.aux0 = static_cast<const float*>(aux0);
+    t.aux1 = static_cast<const float*>(aux1);
+    t.aux_is_lse = aux_is_lse;
+    t.dq = dq;
+    t.dk = dk;
+    t.dv = dv;
+    t.delta = softmax_d != nullptr
+                  ? static_cast<float*>(softmax_d)
+                  : reinterpret_cast<float*>(static_cast<char*>(params->workspace) + plan.delta_off);
+    if (params->reserved_i32[15] == fa3::kStageEventTag) {
+        for (int i = 0; i < 4; ++i) {
+            t.stage_events[i] = static_cast<hipEvent_t>(params->reserved_ptr[4 + i]);
+        }
+    }
+    return finish(fa3::launch_backward(pr, t, params->workspace), params);
+}
+
+size_t workspace_bytes_of(const ShaoboFa3Params* params) {
+    if (validate(params) != SHAOBO_FA3_STATUS_SUCCESS) return 0;
+    const fa3::WorkspacePlan plan = fa3::plan_workspace(problem_of(params));
+    return plan.ok ? plan.total : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+void shaobo_fa3_params_init(ShaoboFa3Params* params) {
+    if (params == nullptr) return;
+    std::memset(params, 0, sizeof(*params));
+    params->struct_size = sizeof(*params);
+    params->window_left = -1;
+    params->window_right = -1;
+    params->dtype = SHAOBO_FA3_DTYPE_FP16;
+    params->layout = SHAOBO_FA3_LAYOUT_BHSD;
+    params->softmax_aux_mode = SHAOBO_FA3_SOFTMAX_AUX_LSE;
+}
+
+int shaobo_fa3_bwd_get_capabilities(ShaoboFa3BwdCapabilities* caps) {
+    if (caps == nullptr || caps->struct_size < sizeof(ShaoboFa3BwdCapabilities)) {
+        return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    }
+    caps->api_version = SHAOBO_FA3_API_VERSION;
+    caps->feature_mask = SHAOBO_FA3_BWD_FEATURE_FIXED_LENGTH | SHAOBO_FA3_BWD_FEATURE_FP16 |
+                         SHAOBO_FA3_BWD_FEATURE_CAUSAL | SHAOBO_FA3_BWD_FEATURE_GQA |
+                         SHAOBO_FA3_BWD_FEATURE_DETERMINISTIC |
+                         SHAOBO_FA3_BWD_FEATURE_SOFTMAX_LSE | SHAOBO_FA3_BWD_FEATURE_BHSD |
+                         SHAOBO_FA3_BWD_FEATURE_FULL_ATTENTION;
+    caps->min_head_dim = kMinHeadDim;
+    caps->max_head_dim = kMaxHeadDim;
+    caps->head_dim_alignment = kMinHeadDim;
+    caps->sequence_alignment = kSequenceAlignment;
+    return SHAOBO_FA3_STATUS_SUCCESS;
+}
+
+int shaobo_fa3_bwd_v2_validate(const ShaoboFa3Params* params) { return validate(params); }
+
+size_t shaobo_fa3_bwd_v2_workspace_bytes(const ShaoboFa3Params* params) {
+    return workspace_bytes_of(params);
+}
+
+int shaobo_fa3_bwd_v2(const void* dout, const void* q, const void* k, const void* v,
+                      const void* out, const void* softmax_lse, void* dq, void* dk, void* dv,
+                      void* softmax_d, const ShaoboFa3Params* params) {
+    return run_backward(dout, q, k, v, out, softmax_lse, nullptr, true, dq, dk, dv, softmax_d,
+                        params);
+}
+
+const char* shaobo_fa3_status_string(int status) {
+    switch (status) {
+        case SHAOBO_FA3_STATUS_SUCCESS: return "success";
+        case SHAOBO_FA3_STATUS_INVALID_VALUE: return "invalid_value";
+        case SHAOBO_FA3_STATUS_UNSUPPORTED: return "unsupported";
+        case SHAOBO_FA3_STATUS_NOT_IMPLEMENTED: return "not_implemented";
+        case SHAOBO_FA3_STATUS_HIP_ERROR: return "hip_error";
+        default: return "unknown";
+    }
+}
+
+size_t shaobo_fa3_bwd_workspace_bytes(const ShaoboFa3Params* params) {
+    return workspace_bytes_of(params);
+}
+
+int shaobo_fa3_bwd(const void* dout, const void* q, const void* k, const void* v,
+                   const void* out, const void* softmax_aux0, const void* softmax_aux1, void* dq,
+                   void* dk, void* dv, const ShaoboFa3Params* params) {
+    if (params == nullptr) return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    const int mode = params->softmax_aux_mode;
+    if (mode != SHAOBO_FA3_SOFTMAX_AUX_LSE && mode != SHAOBO_FA3_SOFTMAX_AUX_SMAX_SSUM) {
+        return validate(params) == SHAOBO_FA3_STATUS_SUCCESS ? SHAOBO_FA3_STATUS_UNSUPPORTED
+                                                              : validate(params);
+    }
+    return run_backward(dout, q, k, v, out, softmax_aux0, softmax_aux1,
+                        mode == SHAOBO_FA3_SOFTMAX_AUX_LSE, dq, dk, dv, nullptr, params);
+}
+
+// ---- component entries (include/shaobo_fa3_components.h) ----
+
+int shaobo_fa3_bwd_dot_do_o(const void* dout, const void* out, const void* softmax_aux0,
+                            const void* softmax_aux1, void* delta, void* packed_sidecar,
+                            const ShaoboFa3Params* params) {
+    // Same acceptance as the reference component (src/dot_do_o_kernel.cpp:65-94):
+    // shape/dtype/layout/aux-mode checks only, then pointer checks.
+    if (params == nullptr || params->batch <= 0 || params->seqlen_q <= 0 ||
+        params->num_heads_q <= 0 || !head_dim_supported(params->head_dim_qk) ||
+        params->head_dim_v != params->head_dim_qk || params->dtype != SHAOBO_FA3_DTYPE_FP16 ||
+        params->layout != SHAOBO_FA3_LAYOUT_BHSD ||
+        (params->softmax_aux_mode != SHAOBO_FA3_SOFTMAX_AUX_SMAX_SSUM &&
+         params->softmax_aux_mode != SHAOBO_FA3_SOFTMAX_AUX_LSE)) {
+        return SHAOBO_FA3_STATUS_UNSUPPORTED;
+    }
+    const bool lse = params->softmax_aux_mode == SHAOBO_FA3_SOFTMAX_AUX_LSE;
+    if (dout == nullptr || out == nullptr || softmax_aux0 == nullptr ||
+        (!lse && softmax_aux1 == nullptr) || delta == nullptr || packed_sidecar == nullptr) {
+        return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    }
+    fa3::BwdProblem pr;
+    pr.batch = params->batch;
+    pr.seqlen = params->seqlen_q;
+    pr.heads_q = params->num_heads_q;
+    pr.heads_kv = params->num_heads_q;
+    pr.head_dim = params->head_dim_qk;
+    pr.scale = params->softmax_scale;
+    fa3::BwdTensors t;
+    t.dout = dout;
+    t.out = out;
+    t.aux0 = static_cast<const float*>(softmax_aux0);
+    t.aux1 = static_cast<const float*>(softmax_aux1);
+    t.aux_is_lse = lse;
+    t.delta = static_cast<float*>(delta);
+    t.packed = static_cast<float*>(packed_sidecar);
+    return finish(fa3::launch_preprocess(pr, t, nullptr, nullptr), params);
+}
+
+}  // extern "C"

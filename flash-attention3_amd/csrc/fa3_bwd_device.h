@@ -1,0 +1,93 @@
+// Device-side building blocks for the gfx950 FlashAttention-3 backward:
+// vector types, the two MFMA shapes used, LDS transposed reads and the
+// bank-conflict-free LDS swizzles of the Q/dO tiles and the dS^T tile.
+//
+// Lane layouts (verified on MI355X by an in-bounds probe of the builtins):
+//   v_mfma_f32_32x32x16_f16   lane l, h = l / 32:
+//     A[m][k]: m = l % 32, k = 8h + t (t = 0..7, the 8 halves of the operand)
+//     B[k][n]: n = l % 32, k = 8h + t
+//     C[m][n]: n = l % 32, m = 8 * (i / 4) + 4h + (i % 4)  (i = 0..15)
+//   ds_read_b64_tr_b16, per group of 16 lanes (r = lane % 16), with A_i the
+//     element address supplied by lane i of the group:
+//     result[r][j] = lds16[A_{4j + r/4} + (r % 4)]   (j = 0..3)
+//     i.e. if lane i points at row (i >> 2), column c0 + 4 * (i & 3) of a
+//     row-major 16-bit matrix, lane r receives column c0 + r of those 4 rows.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa3 {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define FA3_LDS __attribute__((address_space(3)))
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.44269504088896340736f;
+
+__device__ __forceinline__ f32x16 mfma_32x32x16(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Transposed 4 x 16-bit read; `byte_off` is the LDS byte address this lane
+// supplies (see the layout note at the top of the file).
+__device__ __forceinline__ f16x4 lds_read_tr4(const FA3_LDS char* lds, uint32_t byte_off) {
+    typedef __fp16 raw4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+    raw4 r = __builtin_amdgcn_ds_read_tr16_b64_v4f16((FA3_LDS raw4*)(lds + byte_off));
+    return __builtin_bit_cast(f16x4, r);
+}
+
+__device__ __forceinline__ f16x8 concat4(f16x4 lo, f16x4 hi) {
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__device__ __forceinline__ f16x8 lds_read_b128(const FA3_LDS char* lds, uint32_t byte_off) {
+    return *(const FA3_LDS f16x8*)(lds + byte_off);
+}
+
+__device__ __forceinline__ void lds_write_b128(FA3_LDS char* lds, uint32_t byte_off, f16x8 v) {
+    *(FA3_LDS f16x8*)(lds + byte_off) = v;
+}
+
+__device__ __forceinline__ void lds_write_b64(FA3_LDS char* lds, uint32_t byte_off, f16x4 v) {
+    *(FA3_LDS f16x4*)(lds + byte_off) = v;
+}
+
+// Swizzle of a 128-byte row (8 chunks of 16 B, two rows per 64-bank line):
+// rows of equal parity get distinct 3-bit masks over 8 consecutive rows, and
+// rows r, r + 2 (r % 4 == 0) differ in bit 2, so 4 rows x 4 consecutive
+// chunks of a transposed read land on 16 distinct 4-bank windows.
+__device__ __forceinline__ int swz128(int row) {
+    return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
+}
+
+// Row-major [rows][D] fp16 tile with 16-byte chunks XOR-swizzled per row.
+// For D = 128 (16 chunks, one row per 64-bank line) the mask
+// 4 * (r % 4) + (r / 4) % 4 makes both access patterns conflict free:
+// 16 consecutive rows reading one logical chunk (ds_read_b128), and 4
+// consecutive rows x 4 consecutive chunks (ds_read_b64_tr_b16, 32 lanes).
+template <int D>
+__device__ __forceinline__ uint32_t tile_off(int row, int chunk) {
+    constexpr int kChunks = D / 8;
+    static_assert(kChunks == 16 || kChunks == 8, "head dim 64 or 128");
+    int sw;
+    if constexpr (kChunks == 16) {
+        sw = ((row & 3) << 2) | ((row >> 2) & 3);
+    } else {
+        sw = swz128(row);
+    }
+    return (uint32_t)(row * (D * 2) + ((chunk ^ sw) & (kChunks - 1)) * 16);
+}
+
+// dS^T tile [keys][64 queries] fp16: 8 chunks of 16 B per key row.
+__device__ __forceinline__ uint32_t dst_off(int key, int chunk) {
+    return (uint32_t)(key * 128 + ((chunk ^ swz128(key)) & 7) * 16);
+}
+
+}  // namespace fa3

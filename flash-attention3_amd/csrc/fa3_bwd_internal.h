@@ -1,0 +1,71 @@
+// Host-side launch interface between the C ABI layer (fa3_bwd_api.cpp) and
+// the HIP kernels.  Nothing here is exported from the shared library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fa3 {
+
+// Keys owned by one workgroup of the main kernel, and query rows it consumes
+// per pipeline step.  The main kernel tiles both sequence axes by 64.
+constexpr int kTileN = 64;
+constexpr int kTileM = 64;
+
+// Everything a backward launch needs, already validated and resolved
+// (default scale applied, aux mode folded into the lse2 preprocessing).
+struct BwdProblem {
+    int batch = 0;
+    int seqlen = 0;     // Sq == Sk
+    int heads_q = 0;
+    int heads_kv = 0;
+    int head_dim = 0;   // Dqk == Dv, 64 or 128
+    bool causal = false;
+    bool deterministic = false;
+    float scale = 0.f;  // softmax scale
+};
+
+struct BwdTensors {
+    const void* dout = nullptr;
+    const void* q = nullptr;
+    const void* k = nullptr;
+    const void* v = nullptr;
+    const void* out = nullptr;
+    const float* aux0 = nullptr;   // LSE (natural log) or raw row max
+    const float* aux1 = nullptr;   // row sum (SMAX_SSUM mode) or nullptr
+    bool aux_is_lse = true;
+    void* dq = nullptr;
+    void* dk = nullptr;
+    void* dv = nullptr;
+    float* delta = nullptr;        // fp32 rows, written by the preprocess
+    float* packed = nullptr;       // optional [rows][3] sidecar
+    // Optional profiling events recorded on the null stream at the stage
+    // boundaries: before preprocess, before main, before dQ finalize, after.
+    hipEvent_t stage_events[4] = {nullptr, nullptr, nullptr, nullptr};
+};
+
+// params->reserved_i32[15] == kStageEventTag enables stage_events, taken
+// from params->reserved_ptr[4..7] (the reference leaves these unused on v2).
+constexpr int32_t kStageEventTag = 0x53544745;
+
+// Workspace carve-up (all offsets 256-byte aligned).
+struct WorkspacePlan {
+    size_t dq_acc_off = 0, dq_acc_bytes = 0;  // fp32 dQ accumulator / partials
+    size_t lse2_off = 0;                      // fp32 rows: log2-domain LSE
+    size_t delta_off = 0;                     // fp32 rows: internal delta
+    size_t total = 0;
+    bool ok = false;
+};
+
+WorkspacePlan plan_workspace(const BwdProblem& p);
+
+// Launches the whole lifecycle on the null stream:
+// preprocess (delta, lse2, dQ accumulator clear) -> main -> dQ finalize.
+hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace);
+
+// Preprocess only (the component entry shaobo_fa3_bwd_dot_do_o).
+hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
+                             float* dq_acc_to_clear);
+
+}  // namespace fa3

@@ -1,0 +1,96 @@
+// Delta preprocess of the FA3 backward (replaces reference
+// src/dot_do_o_kernel.cpp:26-63 `dot_do_o_kernel`).
+//
+// Per query row r of [B, Hq, S]:
+//   delta[r] = sum_d fp32(dO[r, d]) * fp32(O[r, d])          (fp32)
+//   lse2[r]  = LSE[r] * log2(e)                                 (LSE input)
+//            = max[r] * scale * log2(e) + log2(sum[r])          (SMAX_SSUM)
+// so the main kernel forms P = exp2(s * scale * log2(e) - lse2[r]).
+// Optionally also writes the reference's packed sidecar
+// [row_max_log2, row_inv_sum, delta] (reference src/dot_do_o_kernel.cpp:49-61)
+// and clears the fp32 dQ accumulator rows that the main kernel adds into.
+//
+// HBM-bound: one 16-byte load of dO and of O per lane (D / 8 lanes per row),
+// an in-register dot, and a butterfly reduction over the row's lanes.
+#include "fa3_bwd_device.h"
+#include "fa3_bwd_internal.h"
+
+namespace fa3 {
+namespace {
+
+template <int D, bool kLse>
+__global__ __launch_bounds__(256) void preprocess_kernel(
+    const _Float16* __restrict__ dout, const _Float16* __restrict__ out,
+    const float* __restrict__ aux0, const float* __restrict__ aux1,
+    float* __restrict__ delta, float* __restrict__ lse2, float* __restrict__ packed,
+    float* __restrict__ dq_acc, int rows, float scale_log2) {
+    constexpr int kLanesPerRow = D / 8;
+    constexpr int kRowsPerBlock = 256 / kLanesPerRow;
+    const int sub = threadIdx.x % kLanesPerRow;
+    const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
+    if (row >= rows) return;  // rows % kRowsPerBlock may be non-zero only at the tail
+
+    const size_t base = (size_t)row * D + sub * 8;
+    const f16x8 a = *(const f16x8*)(dout + base);
+    const f16x8 b = *(const f16x8*)(out + base);
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += (float)a[i] * (float)b[i];
+#pragma unroll
+    for (int off = kLanesPerRow / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kLanesPerRow);
+
+    if (dq_acc != nullptr) {
+        f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        *(f32x4*)(dq_acc + base) = z;
+        *(f32x4*)(dq_acc + base + 4) = z;
+    }
+    if (sub == 0) {
+        float l2, max_log2, inv_sum;
+        if constexpr (kLse) {
+            l2 = aux0[row] * kLog2e;
+            max_log2 = l2;
+            inv_sum = 1.f;
+        } else {
+            const float s = aux1[row];
+            max_log2 = aux0[row] * scale_log2;
+            inv_sum = s != 0.f ? 1.f / s : 0.f;
+            l2 = max_log2 + log2f(s);
+        }
+        delta[row] = acc;
+        if (lse2 != nullptr) lse2[row] = l2;
+        if (packed != nullptr) {
+            packed[(size_t)row * 3 + 0] = max_log2;
+            packed[(size_t)row * 3 + 1] = inv_sum;
+            packed[(size_t)row * 3 + 2] = acc;
+        }
+    }
+}
+
+template <int D>
+hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, float* dq_acc) {
+    constexpr int kRowsPerBlock = 256 / (D / 8);
+    const int rows = p.batch * p.heads_q * p.seqlen;
+    const int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    const float scale_log2 = p.scale * kLog2e;
+    if (t.aux_is_lse) {
+        hipLaunchKernelGGL((preprocess_kernel<D, true>), dim3(blocks), dim3(256), 0, 0,
+                           (const _Float16*)t.dout, (const _Float16*)t.out, t.aux0, t.aux1,
+                           t.delta, lse2, t.packed, dq_acc, rows, scale_log2);
+    } else {
+        hipLaunchKernelGGL((preprocess_kernel<D, false>), dim3(blocks), dim3(256), 0, 0,
+                           (const _Float16*)t.dout, (const _Float16*)t.out, t.aux0, t.aux1,
+                           t.delta, lse2, t.packed, dq_acc, rows, scale_log2);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
+                             float* dq_acc_to_clear) {
+    if (p.head_dim == 128) return launch_pre_d<128>(p, t, lse2, dq_acc_to_clear);
+    if (p.head_dim == 64) return launch_pre_d<64>(p, t, lse2, dq_acc_to_clear);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace fa3

@@ -1,0 +1,342 @@
+// CPU oracle for the FA3 backward -- TEST INFRASTRUCTURE ONLY.
+//
+// This library is the checker the GPU path is compared against.  Only the
+// tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it;
+// the shipped library (flash-attention3_amd/) never links or calls it.
+//
+// It restates the reference's fp32 CPU golden,
+// reference scripts/generate_full_bwd_golden.py:135-219 (`cpu_backward`),
+// with the LSE derivation of reference src/full_bwd_correctness.cpp:229-233:
+//   score   = Q K^T                                   (fp32)       golden :172
+//   causal: score[i][j] = -inf for j > i                            :163,175
+//   max_i   = max_j score[i][j]                                     :176
+//   pnum    = exp2((score - max_i) * fp32(scale * log2 e)), masked 0 :177-181
+//   sum_i   = fp32(sum_j pnum in fp64)                              :182
+//   P       = pnum / sum_i                                          :183
+//   O       = fp16(P V)                                             :185
+//   delta_i = sum_d dO[i][d] * fp32(O[i][d])           (fp32)       :186-188
+//   dP      = dO V^T                                                :189
+//   dS      = P * (dP - delta_i) * scale                            :190
+//   dQ = dS K,  dK += dS^T Q,  dV += P^T dO  (GQA kv = h / (Hq/Hkv)) :166,196-198
+//   lse_i   = max_i * scale + ln(sum_i)                 full_bwd_correctness.cpp:229-233
+// Inputs (the build's own): Q, K, V, dO ~ N(0,1) from a
+// seeded splitmix64 + Box-Muller stream, rounded to fp16; and the reference's
+// deterministic pattern, generate_full_bwd_golden.py:135-151.
+//
+// Work is split over (head, 64-row block) with std::thread.  dQ/delta come
+// from a per-query-row pass, dK/dV from a per-key-block pass that recomputes
+// P and dS with the same operation order (so both passes see identical P).
+// Dot products use 8 fixed partial sums (vectorisable, deterministic order);
+// the golden's numpy/BLAS order differs, so agreement is to fp32 rounding.
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <thread>
+#include <vector>
+
+#if defined(__F16C__)
+#include <immintrin.h>
+#endif
+
+namespace {
+
+// ---- fp16 <-> fp32 (IEEE binary16, round to nearest even) ----
+float h2f(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1f;
+    const uint32_t man = h & 0x3ff;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {  // subnormal: value = man * 2^-24
+            float f = (float)man * 5.9604644775390625e-08f;
+            std::memcpy(&bits, &f, 4);
+            bits |= sign;
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 112) << 23) | (man << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+uint16_t f2h(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) {  // inf / nan
+        return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+    }
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // rounds to >= 65520 -> inf
+    if (ax < 0x38800000u) {  // below 2^-14: subnormal half (or zero)
+        float af;
+        std::memcpy(&af, &ax, 4);
+        // value / 2^-24, rounded to nearest even integer
+        const float scaled = af * 16777216.0f;
+        const float r = std::nearbyint(scaled);
+        return (uint16_t)(sign | (uint16_t)r);
+    }
+    // normal: keep 10 mantissa bits with RNE on the dropped 13 bits
+    uint32_t mant = ax & 0x7fffffu;
+    uint32_t exp = (ax >> 23) - 112;
+    uint32_t half = (exp << 10) | (mant >> 13);
+    const uint32_t rem = mant & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (half & 1u))) half += 1;  // may carry into exp
+    return (uint16_t)(sign | half);
+}
+
+void to_f32(const uint16_t* src, float* dst, size_t n) {
+    size_t i = 0;
+#if defined(__F16C__)
+    for (; i + 8 <= n; i += 8) {
+        __m128i hv = _mm_loadu_si128((const __m128i*)(src + i));
+        _mm256_storeu_ps(dst + i, _mm256_cvtph_ps(hv));
+    }
+#endif
+    for (; i < n; ++i) dst[i] = h2f(src[i]);
+}
+
+inline float dot(const float* a, const float* b, int n) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int d = 0;
+    for (; d + 8 <= n; d += 8) {
+        for (int l = 0; l < 8; ++l) acc[l] += a[d + l] * b[d + l];
+    }
+    for (; d < n; ++d) acc[d & 7] += a[d] * b[d];
+    return ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+}
+
+inline void axpy(float a, const float* x, float* y, int n) {
+    for (int d = 0; d < n; ++d) y[d] += a * x[d];
+}
+
+struct Shape {
+    int B, Hq, Hkv, S, D, causal;
+    float scale;
+    int bkv_begin, bkv_end;  // subset of flattened (b * Hkv + hkv) groups
+};
+
+template <typename F>
+void parallel_for(int count, int threads, F&& fn) {
+    if (threads <= 1 || count <= 1) {
+        for (int i = 0; i < count; ++i) fn(i);
+        return;
+    }
+    std::vector<std::thread> pool;
+    const int n = threads < count ? threads : count;
+    for (int t = 0; t < n; ++t) {
+        pool.emplace_back([&, t]() {
+            for (int i = t; i < count; i += n) fn(i);
+        });
+    }
+    for (auto& th : pool) th.join();
+}
+
+// Converted fp32 copies of the head slices in the requested subset.
+struct Tensors {
+    std::vector<float> q, k, v, dout, out;
+};
+
+constexpr int kRowBlock = 64;
+
+// Row statistics of query row i against keys [0, S) (causal: [0, i]).
+// Writes the score row into `score` and returns max and fp32(fp64 sum).
+void row_stats(const float* qi, const float* kh, int i, const Shape& s, float scale_log2,
+               float* score, float* pnum, float& mx, float& sm) {
+    const int nk = s.causal ? i + 1 : s.S;
+    mx = -std::numeric_limits<float>::infinity();
+    for (int j = 0; j < nk; ++j) {
+        score[j] = dot(qi, kh + (size_t)j * s.D, s.D);
+        mx = score[j] > mx ? score[j] : mx;
+    }
+    double acc = 0.0;
+    for (int j = 0; j < nk; ++j) {
+        pnum[j] = std::exp2((score[j] - mx) * scale_log2);
+        acc += (double)pnum[j];
+    }
+    sm = (float)acc;
+}
+
+}  // namespace
+
+extern "C" {
+
+// N(0,1) samples rounded to fp16: splitmix64 -> two 53-bit uniforms ->
+// Box-Muller (both outputs used).  Deterministic for a given seed.
+void fa3o_randn_f16(uint16_t* out, size_t n, uint64_t seed) {
+    uint64_t state = seed;
+    auto next = [&state]() {
+        uint64_t z = (state += 0x9e3779b97f4a7c15ull);
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        return z ^ (z >> 31);
+    };
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; i += 2) {
+        const double u1 = ((next() >> 11) + 1.0) * (1.0 / 9007199254740993.0);  // (0, 1]
+        const double u2 = (next() >> 11) * (1.0 / 9007199254740992.0);          // [0, 1)
+        const double rad = std::sqrt(-2.0 * std::log(u1));
+        out[i] = f2h((float)(rad * std::cos(two_pi * u2)));
+        if (i + 1 < n) out[i + 1] = f2h((float)(rad * std::sin(two_pi * u2)));
+    }
+}
+
+// Reference deterministic input pattern
+// (generate_full_bwd_golden.py:135-140): fp16(fp32((idx*mul + 7) % mod - mod/2) * scale).
+void fa3o_pattern_f16(uint16_t* out, size_t n, int64_t mul, int64_t mod, float value_scale) {
+    for (size_t i = 0; i < n; ++i) {
+        const int64_t v = (((int64_t)i * mul + 7) % mod) - (mod / 2);
+        out[i] = f2h((float)v * value_scale);
+    }
+}
+
+void fa3o_f16_to_f32(const uint16_t* src, float* dst, size_t n) { to_f32(src, dst, n); }
+void fa3o_f32_to_f16(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = f2h(src[i]);
+}
+
+// Forward: out (fp16 bits), scores_max, scores_sum, lse (natural log).
+// Only the query heads of kv groups [bkv_begin, bkv_end) are computed.
+void fa3o_forward(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16, int B, int Hq,
+                  int Hkv, int S, int D, int causal, float scale, int bkv_begin, int bkv_end,
+                  uint16_t* out16, float* smax, float* ssum, float* lse, int threads) {
+    const Shape s{B, Hq, Hkv, S, D, causal, scale, bkv_begin, bkv_end};
+    const int G = Hq / Hkv;
+    const float scale_log2 = (float)(scale * (float)1.4426950408889634);
+    const int nheads = (bkv_end - bkv_begin) * G;
+    const int rblocks = S / kRowBlock + (S % kRowBlock ? 1 : 0);
+    const size_t hsz = (size_t)S * D;
+    parallel_for(nheads * rblocks, threads, [&](int item) {
+        const int hl = item / rblocks, rb = item % rblocks;
+        const int bkv = bkv_begin + hl / G;
+        const int bh = (bkv / Hkv) * Hq + (bkv % Hkv) * G + hl % G;
+        std::vector<float> qh(hsz), kh(hsz), vh(hsz), score(S), pnum(S), o(D);
+        to_f32(q16 + (size_t)bh * hsz, qh.data(), hsz);
+        to_f32(k16 + (size_t)bkv * hsz, kh.data(), hsz);
+        to_f32(v16 + (size_t)bkv * hsz, vh.data(), hsz);
+        const int i1 = (rb + 1) * kRowBlock < S ? (rb + 1) * kRowBlock : S;
+        for (int i = rb * kRowBlock; i < i1; ++i) {
+            float mx, sm;
+            row_stats(qh.data() + (size_t)i * D, kh.data(), i, s, scale_log2, score.data(),
+                      pnum.data(), mx, sm);
+            const int nk = causal ? i + 1 : S;
+            std::fill(o.begin(), o.end(), 0.f);
+            for (int j = 0; j < nk; ++j) axpy(pnum[j] / sm, vh.data() + (size_t)j * D, o.data(), D);
+            const size_t row = (size_t)bh * S + i;
+            for (int d = 0; d < D; ++d) out16[row * D + d] = f2h(o[d]);
+            smax[row] = mx;
+            ssum[row] = sm;
+            lse[row] = mx * scale + std::log(sm);
+        }
+    });
+}
+
+// Backward: delta, dq (fp32 [B,Hq,S,D]), dk, dv (fp32 [B,Hkv,S,D]) for the
+// kv groups [bkv_begin, bkv_end).  smax/ssum are the forward row statistics.
+void fa3o_backward(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16,
+                   const uint16_t* out16, const uint16_t* dout16, const float* smax,
+                   const float* ssum, int B, int Hq, int Hkv, int S, int D, int causal,
+                   float scale, int bkv_begin, int bkv_end, float* delta, float* dq, float* dk,
+                   float* dv, int threads) {
+    const Shape s{B, Hq, Hkv, S, D, causal, scale, bkv_begin, bkv_end};
+    const int G = Hq / Hkv;
+    const float scale_log2 = (float)(scale * (float)1.4426950408889634);
+    const size_t hsz = (size_t)S * D;
+    const int ngroups = bkv_end - bkv_begin;
+    const int rblocks = S / kRowBlock + (S % kRowBlock ? 1 : 0);
+
+    // fp32 copies of the subset (per kv group: G query heads + K, V).
+    std::vector<float> Q((size_t)ngroups * G * hsz), DO((size_t)ngroups * G * hsz),
+        O((size_t)ngroups * G * hsz), K((size_t)ngroups * hsz), V((size_t)ngroups * hsz);
+    parallel_for(ngroups, threads, [&](int gl) {
+        const int bkv = bkv_begin + gl;
+        to_f32(k16 + (size_t)bkv * hsz, K.data() + (size_t)gl * hsz, hsz);
+        to_f32(v16 + (size_t)bkv * hsz, V.data() + (size_t)gl * hsz, hsz);
+        for (int gi = 0; gi < G; ++gi) {
+            const int bh = (bkv / Hkv) * Hq + (bkv % Hkv) * G + gi;
+            const size_t dst = ((size_t)gl * G + gi) * hsz;
+            to_f32(q16 + (size_t)bh * hsz, Q.data() + dst, hsz);
+            to_f32(dout16 + (size_t)bh * hsz, DO.data() + dst, hsz);
+            to_f32(out16 + (size_t)bh * hsz, O.data() + dst, hsz);
+        }
+    });
+    auto bh_of = [&](int gl, int gi) {
+        const int bkv = bkv_begin + gl;
+        return (bkv / Hkv) * Hq + (bkv % Hkv) * G + gi;
+    };
+
+    // Pass 1 (per query row): delta, dq.
+    parallel_for(ngroups * G * rblocks, threads, [&](int item) {
+        const int hl = item / rblocks, rb = item % rblocks;
+        const int gl = hl / G, gi = hl % G;
+        const int bh = bh_of(gl, gi);
+        const float* qh = Q.data() + (size_t)hl * hsz;
+        const float* doh = DO.data() + (size_t)hl * hsz;
+        const float* oh = O.data() + (size_t)hl * hsz;
+        const float* kh = K.data() + (size_t)gl * hsz;
+        const float* vh = V.data() + (size_t)gl * hsz;
+        std::vector<float> score(S), acc(D);
+        const int i1 = (rb + 1) * kRowBlock < S ? (rb + 1) * kRowBlock : S;
+        for (int i = rb * kRowBlock; i < i1; ++i) {
+            const size_t row = (size_t)bh * S + i;
+            const float mx = smax[row], sm = ssum[row];
+            const float* doi = doh + (size_t)i * D;
+            // delta in fp32, sequential over d (numpy fp32 sum order differs)
+            float dl = 0.f;
+            for (int d = 0; d < D; ++d) dl += doi[d] * oh[(size_t)i * D + d];
+            delta[row] = dl;
+            const int nk = causal ? i + 1 : S;
+            std::fill(acc.begin(), acc.end(), 0.f);
+            for (int j = 0; j < nk; ++j) {
+                const float sc = dot(qh + (size_t)i * D, kh + (size_t)j * D, D);
+                const float p = std::exp2((sc - mx) * scale_log2) / sm;
+                const float dp = dot(doi, vh + (size_t)j * D, D);
+                const float ds = p * (dp - dl) * scale;
+                axpy(ds, kh + (size_t)j * D, acc.data(), D);
+            }
+            std::memcpy(dq + row * D, acc.data(), sizeof(float) * D);
+        }
+    });
+
+    // Pass 2 (per key block): dk, dv summed over the G query heads.
+    parallel_for(ngroups * rblocks, threads, [&](int item) {
+        const int gl = item / rblocks, kb = item % rblocks;
+        const int bkv = bkv_begin + gl;
+        const float* kh = K.data() + (size_t)gl * hsz;
+        const float* vh = V.data() + (size_t)gl * hsz;
+        const int j0 = kb * kRowBlock;
+        const int j1 = j0 + kRowBlock < S ? j0 + kRowBlock : S;
+        std::vector<float> dka((size_t)(j1 - j0) * D, 0.f), dva((size_t)(j1 - j0) * D, 0.f);
+        for (int gi = 0; gi < G; ++gi) {
+            const int hl = gl * G + gi;
+            const int bh = bh_of(gl, gi);
+            const float* qh = Q.data() + (size_t)hl * hsz;
+            const float* doh = DO.data() + (size_t)hl * hsz;
+            for (int i = causal ? j0 : 0; i < S; ++i) {
+                const size_t row = (size_t)bh * S + i;
+                const float mx = smax[row], sm = ssum[row], dl = delta[row];
+                const float* qi = qh + (size_t)i * D;
+                const float* doi = doh + (size_t)i * D;
+                const int jend = causal ? (i + 1 < j1 ? i + 1 : j1) : j1;
+                for (int j = j0; j < jend; ++j) {
+                    const float sc = dot(qi, kh + (size_t)j * D, D);
+                    const float p = std::exp2((sc - mx) * scale_log2) / sm;
+                    const float dp = dot(doi, vh + (size_t)j * D, D);
+                    const float ds = p * (dp - dl) * scale;
+                    axpy(ds, qi, dka.data() + (size_t)(j - j0) * D, D);
+                    axpy(p, doi, dva.data() + (size_t)(j - j0) * D, D);
+                }
+            }
+        }
+        std::memcpy(dk + ((size_t)bkv * S + j0) * D, dka.data(), dka.size() * sizeof(float));
+        std::memcpy(dv + ((size_t)bkv * S + j0) * D, dva.data(), dva.size() * sizeof(float));
+    });
+}
+
+}  // extern "C"
