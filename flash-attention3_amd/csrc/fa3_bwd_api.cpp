@@ -150,9 +150,7 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
     t.dq = dq;
     t.dk = dk;
     t.dv = dv;
-    t.delta = softmax_d != nullptr
-                  ? static_cast<float*>(softmax_d)
-                  : reinterpret_cast<float*>(static_cast<char*>(params->workspace) + plan.delta_off);
+    t.delta = static_cast<float*>(softmax_d);
     if (params->reserved_i32[15] == fa3::kStageEventTag) {
         for (int i = 0; i < 4; ++i) {
             t.stage_events[i] = static_cast<hipEvent_t>(params->reserved_ptr[4 + i]);

@@ -38,7 +38,7 @@ struct BwdTensors {
     void* dq = nullptr;
     void* dk = nullptr;
     void* dv = nullptr;
-    float* delta = nullptr;        // fp32 rows, written by the preprocess
+    float* delta = nullptr;        // fp32 rows (softmax_d); may be null
     float* packed = nullptr;       // optional [rows][3] sidecar
     // Optional profiling events recorded on the null stream at the stage
     // boundaries: before preprocess, before main, before dQ finalize, after.
@@ -49,22 +49,18 @@ struct BwdTensors {
 // from params->reserved_ptr[4..7] (the reference leaves these unused on v2).
 constexpr int32_t kStageEventTag = 0x53544745;
 
-// Workspace carve-up (all offsets 256-byte aligned).
+// Device workspace the v2 entry asks the caller for.
 struct WorkspacePlan {
-    size_t dq_acc_off = 0, dq_acc_bytes = 0;  // fp32 dQ accumulator / partials
-    size_t lse2_off = 0;                      // fp32 rows: log2-domain LSE
-    size_t delta_off = 0;                     // fp32 rows: internal delta
     size_t total = 0;
     bool ok = false;
 };
 
 WorkspacePlan plan_workspace(const BwdProblem& p);
 
-// Launches the whole lifecycle on the null stream:
-// preprocess (delta, lse2, dQ accumulator clear) -> main -> dQ finalize.
+// Launches the whole backward (one fused kernel) on the null stream.
 hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace);
 
-// Preprocess only (the component entry shaobo_fa3_bwd_dot_do_o).
+// Delta preprocess only (the component entry shaobo_fa3_bwd_dot_do_o).
 hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
                              float* dq_acc_to_clear);
 
