@@ -17,6 +17,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace fa3 {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));

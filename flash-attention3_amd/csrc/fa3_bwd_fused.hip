@@ -1,10 +1,11 @@
-// The FA3 backward for gfx950 in one launch (replaces the reference's
-// delta preprocess + fused 5-GEMM kernel + dQ / dKV reductions:
-// src/dot_do_o_kernel.cpp:26-63, src/fused_bwd_kernel.cpp:1362-1671,
+// Main FA3 backward kernel for gfx950 (replaces the reference's fused 5-GEMM
+// kernel and its dQ / GQA-dKV reductions: src/fused_bwd_kernel.cpp:1362-1671,
 // src/fused_bwd_dq_reduce.cpp:27-109, and the legacy dKV / dQ kernels
-// src/dkv_kernel.cpp:957-1085, src/dq_kernel.cpp:794-953).
+// src/dkv_kernel.cpp:957-1085, src/dq_kernel.cpp:794-953).  It runs after the
+// delta preprocess (fa3_bwd_preprocess.hip), which supplies per query row
+// delta = rowsum(dO * O) and lse2 = LSE * log2(e).
 //
-// Two workgroup roles share the grid, so no workgroup ever adds into memory
+// Two workgroup roles share one grid, and no workgroup ever adds into memory
 // another one writes (no atomics, no partial buffers, bitwise deterministic):
 //
 //  * dKV role -- owns a 64-key tile of one KV head; streams every 64-row query
@@ -16,18 +17,18 @@
 //    tiles it sees, recomputing S^T and dP^T, and accumulates dQ^T:
 //        S^T = K Q^T, dP^T = V dO^T, dS^T, dQ^T += K^T dS^T (3 GEMMs per tile)
 //
-// Both roles compute delta = rowsum(dO * O) themselves from the tiles they
-// load (same fp32 operation order in both, so the values agree bitwise); the
-// dQ role also writes it to softmax_d.  lse2 = LSE * log2(e) (or, for the
-// legacy max/sum input, max * scale * log2(e) + log2(sum)).  The softmax scale
-// is folded out of dS and applied once to dK and dQ.
+// The softmax scale is folded out of dS and applied once to dK and dQ.
 //
 // Wave layout: 4 waves, wave w = (w & 1, w >> 1) = (key half, query half) in
 // the dKV role and (query half, key half) in the dQ role; each wave works on
 // a 32 x 32 score block with v_mfma_f32_32x32x16_f16.  The two waves that
 // share an output block add their partials through LDS once at the end.
-// Streamed tiles are double-buffered in LDS and filled with direct-to-LDS
-// loads (global_load_lds_dwordx4) one tile ahead of use.
+//
+// Pipeline: streamed tiles live in four LDS buffers filled by direct-to-LDS
+// loads (global_load_lds_dwordx4) issued three tiles ahead; iteration `it`
+// runs the softmax of tile it (VALU) beside S/dP of tile it+1 (MFMA), then
+// the dV/dK (or dQ) MFMAs of tile it.  Waits use explicit vmcnt values so the
+// loads of the following tile stay in flight across the barrier.
 #include "fa3_bwd_device.h"
 #include "fa3_bwd_internal.h"
 
@@ -39,13 +40,11 @@ struct FusedArgs {
     const _Float16* k;
     const _Float16* v;
     const _Float16* dout;
-    const _Float16* out;
-    const float* aux0;
-    const float* aux1;
+    const float* lse2;   // [B*Hq*S]
+    const float* delta;  // [B*Hq*S]
     _Float16* dq;
     _Float16* dk;
     _Float16* dv;
-    float* delta_out;  // may be null
     int seqlen;
     int heads_q;
     int heads_kv;
@@ -56,6 +55,8 @@ struct FusedArgs {
     float scale;
 };
 
+constexpr int kNBuf = 4;
+
 template <int D>
 struct Cfg {
     static constexpr int kTileBytes = 64 * D * 2;          // one [64][D] fp16 tile
@@ -63,53 +64,54 @@ struct Cfg {
     static constexpr int kMB = D / 32;                     // 32-row blocks of D
     static constexpr int kChunks = D / 8;                  // 16-byte chunks per row
     static constexpr int kLoadsPerWave = kTileBytes / 1024 / 4;
-    // dKV role: per buffer Q, dO, O tiles; then wave-private delta/lse2 rows.
-    static constexpr int kKvBuf = 3 * kTileBytes;
-    static constexpr int kKvPriv = 2 * kKvBuf;
-    static constexpr int kKvBytes = kKvPriv + 4 * 2 * 32 * 4;
-    // dQ role: per buffer K, V tiles.
+    // dKV role buffer: Q tile, dO tile, lse2[64], delta[64]
+    static constexpr int kKvRows = 2 * kTileBytes;
+    static constexpr int kKvBuf = kKvRows + 2 * 64 * 4;
+    // dQ role buffer: K tile, V tile
     static constexpr int kQBuf = 2 * kTileBytes;
-    static constexpr int kQBytes = 2 * kQBuf;
-    static constexpr int kBytes = kKvBytes > kQBytes ? kKvBytes : kQBytes;
+    static constexpr int kBytes = kNBuf * (kKvBuf > kQBuf ? kKvBuf : kQBuf);
     // final cross-wave exchange: 2 waves x kMB x 16 x 64 floats
-    static_assert(2 * kMB * 16 * 64 * 4 <= 2 * kTileBytes, "exchange fits in the tiles");
+    static_assert(2 * kMB * 16 * 64 * 4 <= kBytes, "exchange fits in the buffers");
 };
 
-// Direct-to-LDS copy of rows [row0, row0 + 64) of a row-major [*, D] fp16
-// tensor into a swizzled [64][D] LDS tile; every wave moves kLoadsPerWave KB.
+// s_waitcnt vmcnt(N) leaving the LDS and export counters alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// Direct-to-LDS copy of a row-major [64][D] fp16 tile into a swizzled LDS
+// tile.  Lane `lane` of wave `wave` moves the 16-byte chunk that belongs at
+// LDS byte blk * 1024 + lane * 16 (blk = wave * kLoadsPerWave + j); its
+// source byte offset within the global tile is precomputed once.
 template <int D>
-__device__ __forceinline__ void load_tile_async(FA3_LDS char* tile, const _Float16* src, int wave,
-                                                int lane) {
+__device__ __forceinline__ void tile_load_offsets(uint32_t (&off)[Cfg<D>::kLoadsPerWave],
+                                                  int wave, int lane) {
     using C = Cfg<D>;
 #pragma unroll
     for (int j = 0; j < C::kLoadsPerWave; ++j) {
-        const int blk = wave * C::kLoadsPerWave + j;       // 1 KB block of the tile
-        const int id = blk * 64 + lane;                    // physical 16-byte chunk
+        const int id = (wave * C::kLoadsPerWave + j) * 64 + lane;  // physical chunk
         const int row = id / C::kChunks;
         const int phys = id % C::kChunks;
         int sw;
         if constexpr (C::kChunks == 16) sw = ((row & 3) << 2) | ((row >> 2) & 3);
         else sw = swz128(row);
         const int logical = (phys ^ sw) & (C::kChunks - 1);
-        __builtin_amdgcn_global_load_lds((const void*)(src + row * D + logical * 8),
-                                         (FA3_LDS void*)(tile + blk * 1024), 16, 0, 0);
+        off[j] = (uint32_t)((row * D + logical * 8) * 2);
     }
 }
 
-__device__ __forceinline__ float fdot8(f16x8 a, f16x8 b, float acc) {
+template <int D>
+__device__ __forceinline__ void load_tile_async(FA3_LDS char* tile, const _Float16* src,
+                                                const uint32_t (&off)[Cfg<D>::kLoadsPerWave],
+                                                int wave) {
+    using C = Cfg<D>;
 #pragma unroll
-    for (int t = 0; t < 8; t += 2) {
-        acc = __builtin_amdgcn_fdot2(f16x2{a[t], a[t + 1]}, f16x2{b[t], b[t + 1]}, acc, false);
-    }
-    return acc;
-}
-
-template <bool kLse>
-__device__ __forceinline__ float lse2_of(const FusedArgs& a, size_t row) {
-    if constexpr (kLse) {
-        return a.aux0[row] * kLog2e;
-    } else {
-        return a.aux0[row] * a.scale_log2 + __builtin_amdgcn_logf(a.aux1[row]);
+    for (int j = 0; j < C::kLoadsPerWave; ++j) {
+        __builtin_amdgcn_global_load_lds((const void*)((const char*)src + off[j]),
+                                         (FA3_LDS void*)(tile + (wave * C::kLoadsPerWave + j) * 1024),
+                                         16, 0, 0);
     }
 }
 
@@ -118,7 +120,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // ----------------------------------------------------------------------------
 // dKV role
 // ----------------------------------------------------------------------------
-template <int D, bool kCausal, bool kLse>
+template <int D, bool kCausal>
 __device__ void dkv_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
     using C = Cfg<D>;
     const int tid = threadIdx.x;
@@ -155,80 +157,76 @@ __device__ void dkv_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
     const int qt0 = kCausal ? kt : 0;
     const int per_head = QT - qt0;
     const int n_it = group * per_head;
-    const int bhq0 = b * a.heads_q + hkv * group;
-    auto tile_of = [&](int it, int& bhq, int& qt) {
-        bhq = bhq0 + it / per_head;
-        qt = qt0 + it % per_head;
-    };
-    FA3_LDS float* priv = (FA3_LDS float*)(smem + C::kKvPriv) + w * 64;
+    uint32_t ld_off[C::kLoadsPerWave];
+    tile_load_offsets<D>(ld_off, w, lane);
 
-    // prologue: tile 0 in flight, its softmax row statistic in a register
-    int bhq, qt;
-    tile_of(0, bhq, qt);
-    {
-        const size_t base = ((size_t)bhq * S + qt * 64) * D;
-        load_tile_async<D>(smem, a.q + base, w, lane);
-        load_tile_async<D>(smem + C::kTileBytes, a.dout + base, w, lane);
-        load_tile_async<D>(smem + 2 * C::kTileBytes, a.out + base, w, lane);
-    }
-    float l2_cur = lse2_of<kLse>(a, (size_t)bhq * S + qt * 64 + 32 * wq + l32);
-
-    for (int it = 0; it < n_it; ++it) {
-        const int cur_qt = qt;
-        FA3_LDS char* buf = smem + (it & 1) * C::kKvBuf;
-        __syncthreads();  // tile `it` landed; buffer (it+1)&1 no longer read
-        float l2_next = 0.f;
-        if (it + 1 < n_it) {
-            tile_of(it + 1, bhq, qt);
-            const size_t base = ((size_t)bhq * S + qt * 64) * D;
-            FA3_LDS char* nbuf = smem + ((it + 1) & 1) * C::kKvBuf;
-            load_tile_async<D>(nbuf, a.q + base, w, lane);
-            load_tile_async<D>(nbuf + C::kTileBytes, a.dout + base, w, lane);
-            load_tile_async<D>(nbuf + 2 * C::kTileBytes, a.out + base, w, lane);
-            l2_next = lse2_of<kLse>(a, (size_t)bhq * S + qt * 64 + 32 * wq + l32);
+    // Tiles are issued in order; (issue_bhq, issue_qt) is the next one.
+    int issue_bhq = b * a.heads_q + hkv * group;
+    int issue_qt = qt0;
+    auto issue_next = [&](int slot) {
+        const size_t row0 = (size_t)issue_bhq * S + issue_qt * 64;
+        FA3_LDS char* nb = smem + slot * C::kKvBuf;
+        load_tile_async<D>(nb, a.q + row0 * D, ld_off, w);
+        load_tile_async<D>(nb + C::kTileBytes, a.dout + row0 * D, ld_off, w);
+        if (w == 0) {
+            __builtin_amdgcn_global_load_lds((const void*)(a.lse2 + row0 + lane),
+                                             (FA3_LDS void*)(nb + C::kKvRows), 4, 0, 0);
+        } else if (w == 1) {
+            __builtin_amdgcn_global_load_lds((const void*)(a.delta + row0 + lane),
+                                             (FA3_LDS void*)(nb + C::kKvRows + 256), 4, 0, 0);
         }
+        if (++issue_qt == QT) {
+            issue_qt = qt0;
+            ++issue_bhq;
+        }
+    };
+    // vmcnt allowing `tiles` tiles of this wave's loads to stay in flight
+    auto wait_tiles = [&](int tiles) {
+        if (w < 2) {
+            if (tiles >= 2) wait_vmcnt<2 * (2 * C::kLoadsPerWave + 1)>();
+            else if (tiles == 1) wait_vmcnt<2 * C::kLoadsPerWave + 1>();
+            else wait_vmcnt<0>();
+        } else {
+            if (tiles >= 2) wait_vmcnt<2 * (2 * C::kLoadsPerWave)>();
+            else if (tiles == 1) wait_vmcnt<2 * C::kLoadsPerWave>();
+            else wait_vmcnt<0>();
+        }
+    };
 
-        // S = Q K^T, dP = dO V^T (wave: q rows 32wq.., keys 32wk..), and the
-        // lane's half of delta for row 32wq + l32 from the same dO fragments.
-        f32x16 sacc = f32x16{}, pacc = f32x16{};
-        float dpart = 0.f;
+    // S = Q K^T, dP = dO V^T (wave: q rows 32wq.., keys 32wk..)
+    auto stage_a = [&](FA3_LDS char* buf, f32x16& sacc, f32x16& pacc) {
+        sacc = f32x16{};
+        pacc = f32x16{};
 #pragma unroll
         for (int s = 0; s < C::kKSteps; ++s) {
             const uint32_t off = tile_off<D>(32 * wq + l32, 2 * s + h);
-            const f16x8 qa = lds_read_b128(buf, off);
-            const f16x8 da = lds_read_b128(buf + C::kTileBytes, off);
-            const f16x8 oa = lds_read_b128(buf + 2 * C::kTileBytes, off);
-            sacc = mfma_32x32x16(qa, kf[s], sacc);
-            pacc = mfma_32x32x16(da, vf[s], pacc);
-            dpart = fdot8(da, oa, dpart);
+            sacc = mfma_32x32x16(lds_read_b128(buf, off), kf[s], sacc);
+            pacc = mfma_32x32x16(lds_read_b128(buf + C::kTileBytes, off), vf[s], pacc);
         }
-        const float delta_row = dpart + __shfl_xor(dpart, 32);
-        // wave-private broadcast of (delta, lse2) for the wave's 32 rows
-        if (h == 0) {
-            priv[l32] = delta_row;
-            priv[32 + l32] = l2_cur;
-        }
-        __builtin_amdgcn_wave_barrier();
-
-        // P, dS: lane holds key 32wk + l32, q = 32wq + 8(i/4) + 4h + i%4
-        const bool diag = kCausal && (cur_qt == kt);
-        f16x8 pb[2], dsb[2];
+    };
+    // P and dS; lane holds key 32wk + l32, q = 32wq + 8(i/4) + 4h + i%4.
+    auto stage_b = [&](auto masked, const f32x16& sacc, const f32x16& pacc,
+                       const FA3_LDS char* buf, f16x8 (&pb)[2], f16x8 (&dsb)[2]) {
+        const FA3_LDS float* rows = (const FA3_LDS float*)(buf + C::kKvRows);
 #pragma unroll
         for (int a4 = 0; a4 < 4; ++a4) {
-            const f32x4 dl = *(const FA3_LDS f32x4*)(priv + 8 * a4 + 4 * h);
-            const f32x4 l2 = *(const FA3_LDS f32x4*)(priv + 32 + 8 * a4 + 4 * h);
+            const f32x4 l2 = *(const FA3_LDS f32x4*)(rows + 32 * wq + 8 * a4 + 4 * h);
+            const f32x4 dl = *(const FA3_LDS f32x4*)(rows + 64 + 32 * wq + 8 * a4 + 4 * h);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int i = 4 * a4 + e;
                 float p = fast_exp2(sacc[i] * a.scale_log2 - l2[e]);
-                if (diag && (32 * wk + l32 > 32 * wq + 8 * a4 + 4 * h + e)) p = 0.f;
+                if constexpr (decltype(masked)::value) {
+                    if (32 * wk + l32 > 32 * wq + 8 * a4 + 4 * h + e) p = 0.f;
+                }
                 pb[i >> 3][i & 7] = (_Float16)p;
                 dsb[i >> 3][i & 7] = (_Float16)(p * (pacc[i] - dl[e]));
             }
         }
-
-        // dV^T += dO^T P, dK^T += Q^T dS; A operands by transposed reads with
-        // q = 16ks + 8u + 4h + j matching the C-register order of P / dS.
+    };
+    // dV^T += dO^T P, dK^T += Q^T dS; A operands by transposed reads with
+    // q = 16ks + 8u + 4h + j matching the C-register order of P / dS.
+    auto stage_c = [&](FA3_LDS char* buf, const f16x8 (&pb)[2], const f16x8 (&dsb)[2]) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
@@ -246,7 +244,41 @@ __device__ void dkv_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
                 dkt[mb] = mfma_32x32x16(concat4(aq[0], aq[1]), dsb[ks], dkt[mb]);
             }
         }
-        l2_cur = l2_next;
+    };
+    // One pipeline step on tile `it`: softmax of it, S/dP of it+1, dV/dK of
+    // it.  The last step computes S/dP on a stale buffer and drops them, so
+    // every step has the same straight-line body.
+    auto step = [&](auto masked, int it, f32x16& sacc, f32x16& pacc) {
+        const int slot = it & (kNBuf - 1);
+        if (it + 1 < n_it) {
+            wait_tiles(it + 2 < n_it ? 1 : 0);  // tile it+1 landed everywhere
+            __builtin_amdgcn_s_barrier();        // and tile it-1's buffer is free
+            if (it + 3 < n_it) issue_next((it + 3) & (kNBuf - 1));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 pb[2], dsb[2];
+        FA3_LDS char* buf = smem + slot * C::kKvBuf;
+        stage_b(masked, sacc, pacc, buf, pb, dsb);
+        stage_a(smem + ((slot + 1) & (kNBuf - 1)) * C::kKvBuf, sacc, pacc);
+        stage_c(buf, pb, dsb);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // prologue: up to three tiles in flight, S/dP of tile 0
+    const int pre = n_it < 3 ? n_it : 3;
+    for (int i = 0; i < pre; ++i) issue_next(i);
+    wait_tiles(pre - 1);
+    __builtin_amdgcn_s_barrier();
+    f32x16 sacc, pacc;
+    stage_a(smem, sacc, pacc);
+
+    // The causal diagonal is the first query tile of every head in the group.
+    int it = 0;
+    for (int gi = 0; gi < group; ++gi) {
+        if (kCausal) step(std::true_type{}, it, sacc, pacc);
+        else step(std::false_type{}, it, sacc, pacc);
+        ++it;
+        for (int j = 1; j < per_head; ++j, ++it) step(std::false_type{}, it, sacc, pacc);
     }
 
     // Combine the two query-half partials; lane: key 32wk + l32,
@@ -288,7 +320,7 @@ __device__ void dkv_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
 // ----------------------------------------------------------------------------
 // dQ role
 // ----------------------------------------------------------------------------
-template <int D, bool kCausal, bool kLse>
+template <int D, bool kCausal>
 __device__ void dq_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
     using C = Cfg<D>;
     const int tid = threadIdx.x;
@@ -308,20 +340,15 @@ __device__ void dq_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
     const int qbase = qt * 64;
     const size_t row = (size_t)bhq * S + qbase + 32 * wq + l32;
 
-    // B operands of S^T = K Q^T and dP^T = V dO^T: q = row, d = 16s + 8h + t;
-    // delta for the row from the same dO fragments and O.
+    // B operands of S^T = K Q^T and dP^T = V dO^T: q = row, d = 16s + 8h + t
     f16x8 qf[C::kKSteps], df[C::kKSteps];
-    float dpart = 0.f;
 #pragma unroll
     for (int s = 0; s < C::kKSteps; ++s) {
         qf[s] = *(const f16x8*)(a.q + row * D + 16 * s + 8 * h);
         df[s] = *(const f16x8*)(a.dout + row * D + 16 * s + 8 * h);
-        const f16x8 of = *(const f16x8*)(a.out + row * D + 16 * s + 8 * h);
-        dpart = fdot8(df[s], of, dpart);
     }
-    const float delta_row = dpart + __shfl_xor(dpart, 32);
-    const float l2 = lse2_of<kLse>(a, row);
-    if (a.delta_out != nullptr && wk == 0 && h == 0) a.delta_out[row] = delta_row;
+    const float l2 = a.lse2[row];
+    const float delta_row = a.delta[row];
 
     f32x16 dqt[C::kMB];
 #pragma unroll
@@ -330,34 +357,43 @@ __device__ void dq_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
     const int n_kt = kCausal ? qt + 1 : QT;
     const _Float16* kh = a.k + (size_t)bkv * S * D;
     const _Float16* vh = a.v + (size_t)bkv * S * D;
-    load_tile_async<D>(smem, kh, w, lane);
-    load_tile_async<D>(smem + C::kTileBytes, vh, w, lane);
-
-    for (int kt = 0; kt < n_kt; ++kt) {
-        FA3_LDS char* buf = smem + (kt & 1) * C::kQBuf;
-        __syncthreads();
-        if (kt + 1 < n_kt) {
-            FA3_LDS char* nbuf = smem + ((kt + 1) & 1) * C::kQBuf;
-            load_tile_async<D>(nbuf, kh + (size_t)(kt + 1) * 64 * D, w, lane);
-            load_tile_async<D>(nbuf + C::kTileBytes, vh + (size_t)(kt + 1) * 64 * D, w, lane);
-        }
-        // S^T, dP^T: lane holds q = 32wq + l32, key = 32wk + 8(i/4) + 4h + i%4
-        f32x16 sacc = f32x16{}, pacc = f32x16{};
+    uint32_t ld_off[C::kLoadsPerWave];
+    tile_load_offsets<D>(ld_off, w, lane);
+    int issue_kt = 0;
+    auto issue_next = [&](int slot) {
+        FA3_LDS char* nb = smem + slot * C::kQBuf;
+        load_tile_async<D>(nb, kh + (size_t)issue_kt * 64 * D, ld_off, w);
+        load_tile_async<D>(nb + C::kTileBytes, vh + (size_t)issue_kt * 64 * D, ld_off, w);
+        ++issue_kt;
+    };
+    auto wait_tiles = [&](int tiles) {
+        if (tiles >= 2) wait_vmcnt<2 * (2 * C::kLoadsPerWave)>();
+        else if (tiles == 1) wait_vmcnt<2 * C::kLoadsPerWave>();
+        else wait_vmcnt<0>();
+    };
+    // S^T, dP^T: lane holds q = 32wq + l32, key = 32wk + 8(i/4) + 4h + i%4
+    auto stage_a = [&](FA3_LDS char* buf, f32x16& sacc, f32x16& pacc) {
+        sacc = f32x16{};
+        pacc = f32x16{};
 #pragma unroll
         for (int s = 0; s < C::kKSteps; ++s) {
             const uint32_t off = tile_off<D>(32 * wk + l32, 2 * s + h);
             sacc = mfma_32x32x16(lds_read_b128(buf, off), qf[s], sacc);
             pacc = mfma_32x32x16(lds_read_b128(buf + C::kTileBytes, off), df[s], pacc);
         }
-        const bool diag = kCausal && (kt == qt);
-        f16x8 dsb[2];
+    };
+    auto stage_b = [&](auto masked, const f32x16& sacc, const f32x16& pacc, f16x8 (&dsb)[2]) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             float p = fast_exp2(sacc[i] * a.scale_log2 - l2);
-            if (diag && (32 * wk + 8 * (i >> 2) + 4 * h + (i & 3) > 32 * wq + l32)) p = 0.f;
+            if constexpr (decltype(masked)::value) {
+                if (32 * wk + 8 * (i >> 2) + 4 * h + (i & 3) > 32 * wq + l32) p = 0.f;
+            }
             dsb[i >> 3][i & 7] = (_Float16)(p * (pacc[i] - delta_row));
         }
-        // dQ^T += K^T dS^T; A = K^T by transposed reads, key order matching dsb
+    };
+    // dQ^T += K^T dS^T; A = K^T by transposed reads, key order matching dsb
+    auto stage_c = [&](FA3_LDS char* buf, const f16x8 (&dsb)[2]) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
@@ -372,7 +408,33 @@ __device__ void dq_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
                 dqt[mb] = mfma_32x32x16(concat4(ak[0], ak[1]), dsb[ks], dqt[mb]);
             }
         }
-    }
+    };
+
+    auto step = [&](auto masked, int kt, f32x16& sacc, f32x16& pacc) {
+        const int slot = kt & (kNBuf - 1);
+        if (kt + 1 < n_kt) {
+            wait_tiles(kt + 2 < n_kt ? 1 : 0);
+            __builtin_amdgcn_s_barrier();
+            if (kt + 3 < n_kt) issue_next((kt + 3) & (kNBuf - 1));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 dsb[2];
+        stage_b(masked, sacc, pacc, dsb);
+        stage_a(smem + ((slot + 1) & (kNBuf - 1)) * C::kQBuf, sacc, pacc);
+        stage_c(smem + slot * C::kQBuf, dsb);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const int pre = n_kt < 3 ? n_kt : 3;
+    for (int i = 0; i < pre; ++i) issue_next(i);
+    wait_tiles(pre - 1);
+    __builtin_amdgcn_s_barrier();
+    f32x16 sacc, pacc;
+    stage_a(smem, sacc, pacc);
+    // key tiles before the last are below the causal diagonal
+    for (int kt = 0; kt + 1 < n_kt; ++kt) step(std::false_type{}, kt, sacc, pacc);
+    if (kCausal) step(std::true_type{}, n_kt - 1, sacc, pacc);
+    else step(std::false_type{}, n_kt - 1, sacc, pacc);
 
     // Combine the two key-half partials; lane: q = 32wq + l32,
     // d = 32mb + 8(i/4) + 4h + i%4.
@@ -405,7 +467,7 @@ __device__ void dq_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
 
 // Grid: the two roles interleaved, each in longest-first order, so the
 // dispatcher starts the longest jobs first.
-template <int D, bool kCausal, bool kLse>
+template <int D, bool kCausal>
 __global__ __launch_bounds__(256, 1) void bwd_fused_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
@@ -420,46 +482,44 @@ __global__ __launch_bounds__(256, 1) void bwd_fused_kernel(FusedArgs a) {
         kv = a.n_kv_jobs > a.n_q_jobs;
         job = both + (id - 2 * both);
     }
-    if (kv) dkv_role<D, kCausal, kLse>(a, job, smem);
-    else dq_role<D, kCausal, kLse>(a, job, smem);
-}
-
-template <int D, bool kCausal, bool kLse>
-void launch_t(const FusedArgs& a) {
-    hipLaunchKernelGGL((bwd_fused_kernel<D, kCausal, kLse>), dim3(a.n_kv_jobs + a.n_q_jobs),
-                       dim3(256), 0, 0, a);
+    if (kv) dkv_role<D, kCausal>(a, job, smem);
+    else dq_role<D, kCausal>(a, job, smem);
 }
 
 template <int D>
-void launch_d(const FusedArgs& a, bool causal, bool lse) {
-    if (causal) {
-        if (lse) launch_t<D, true, true>(a);
-        else launch_t<D, true, false>(a);
-    } else {
-        if (lse) launch_t<D, false, true>(a);
-        else launch_t<D, false, false>(a);
-    }
+void launch_d(const FusedArgs& a, bool causal) {
+    const dim3 grid(a.n_kv_jobs + a.n_q_jobs);
+    if (causal) hipLaunchKernelGGL((bwd_fused_kernel<D, true>), grid, dim3(256), 0, 0, a);
+    else hipLaunchKernelGGL((bwd_fused_kernel<D, false>), grid, dim3(256), 0, 0, a);
 }
 
 }  // namespace
 
 hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace) {
-    (void)workspace;
     auto mark = [&](int i) {
         if (t.stage_events[i] != nullptr) (void)hipEventRecord(t.stage_events[i], 0);
     };
+    const WorkspacePlan plan = plan_workspace(p);
+    char* ws = static_cast<char*>(workspace);
+    float* lse2 = reinterpret_cast<float*>(ws + plan.lse2_off);
+    BwdTensors pre = t;
+    if (pre.delta == nullptr) pre.delta = reinterpret_cast<float*>(ws + plan.delta_off);
+
+    mark(0);
+    hipError_t err = launch_preprocess(p, pre, lse2, nullptr);
+    if (err != hipSuccess) return err;
+    mark(1);
+
     FusedArgs a;
     a.q = (const _Float16*)t.q;
     a.k = (const _Float16*)t.k;
     a.v = (const _Float16*)t.v;
     a.dout = (const _Float16*)t.dout;
-    a.out = (const _Float16*)t.out;
-    a.aux0 = t.aux0;
-    a.aux1 = t.aux1;
+    a.lse2 = lse2;
+    a.delta = pre.delta;
     a.dq = (_Float16*)t.dq;
     a.dk = (_Float16*)t.dk;
     a.dv = (_Float16*)t.dv;
-    a.delta_out = t.delta;
     a.seqlen = p.seqlen;
     a.heads_q = p.heads_q;
     a.heads_kv = p.heads_kv;
@@ -468,20 +528,21 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     a.n_q_jobs = (p.seqlen / kTileM) * p.batch * p.heads_q;
     a.scale_log2 = p.scale * kLog2e;
     a.scale = p.scale;
-    mark(0);
-    mark(1);
-    if (p.head_dim == 128) launch_d<128>(a, p.causal, t.aux_is_lse);
-    else launch_d<64>(a, p.causal, t.aux_is_lse);
-    const hipError_t err = hipGetLastError();
+    if (p.head_dim == 128) launch_d<128>(a, p.causal);
+    else launch_d<64>(a, p.causal);
+    err = hipGetLastError();
     mark(2);
     mark(3);
     return err;
 }
 
 WorkspacePlan plan_workspace(const BwdProblem& p) {
-    (void)p;
     WorkspacePlan w;
-    w.total = 256;  // reserved; the single-launch path keeps no state in it
+    const size_t rows = (size_t)p.batch * p.heads_q * p.seqlen;
+    auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    w.lse2_off = 0;
+    w.delta_off = align(rows * sizeof(float));
+    w.total = align(w.delta_off + rows * sizeof(float));
     w.ok = true;
     return w;
 }

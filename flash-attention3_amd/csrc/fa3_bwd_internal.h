@@ -49,15 +49,19 @@ struct BwdTensors {
 // from params->reserved_ptr[4..7] (the reference leaves these unused on v2).
 constexpr int32_t kStageEventTag = 0x53544745;
 
-// Device workspace the v2 entry asks the caller for.
+// Device workspace the v2 entry asks the caller for: fp32 lse2 rows, then
+// fp32 delta rows (used when the caller passes no softmax_d), 256-B aligned.
 struct WorkspacePlan {
+    size_t lse2_off = 0;
+    size_t delta_off = 0;
     size_t total = 0;
     bool ok = false;
 };
 
 WorkspacePlan plan_workspace(const BwdProblem& p);
 
-// Launches the whole backward (one fused kernel) on the null stream.
+// Launches the backward on the null stream: delta preprocess, then the
+// main kernel.
 hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace);
 
 // Delta preprocess only (the component entry shaobo_fa3_bwd_dot_do_o).

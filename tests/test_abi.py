@@ -165,15 +165,17 @@ def test_status_strings(lib):
 
 
 def test_workspace_sizes(lib):
-    """The single-launch backward keeps no state in the workspace; v2 still
-    asks for a small non-zero reservation (the reference contract test
-    requires a non-zero size for a supported shape, fused_bwd_api_contract.cpp:60-63)."""
+    """fp32 lse2 rows + fp32 delta rows (delta used when softmax_d is NULL),
+    each region 256-byte aligned; the reference contract test requires a
+    non-zero size for a supported shape (fused_bwd_api_contract.cpp:60-63)."""
     def ws(**kw):
         p = F.make_params(lib, **kw)
         return lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
-    assert ws(batch=1, seqlen=2048, heads_q=4) == 256
-    assert ws(batch=1, seqlen=2048, heads_q=4, deterministic=True) == 256
-    assert ws(batch=2, seqlen=8192, heads_q=16, head_dim=64, causal=False) == 256
+    rows = 1 * 4 * 2048
+    assert ws(batch=1, seqlen=2048, heads_q=4) == 2 * rows * 4
+    assert ws(batch=1, seqlen=2048, heads_q=4, deterministic=True) == 2 * rows * 4
+    assert ws(batch=2, seqlen=8192, heads_q=16, head_dim=64, causal=False) == 2 * 2 * 16 * 8192 * 4
+    assert ws(batch=1, seqlen=128, heads_q=1) == 1024
 
 
 def test_launch_error_paths_without_gpu(lib):
