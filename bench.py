@@ -1,7 +1,7 @@
 """Benchmark of the FA3 backward (shaobo_fa3_bwd_v2) on one MI355X.
 
-A step is one full backward lifecycle (delta preprocess -> main kernel -> dQ
-finalize) through the C ABI over resident fp16 inputs at the headline shape
+A step is one full backward (delta preprocess kernel -> main kernel) through
+the C ABI over resident fp16 inputs at the headline shape
 B=1, H=4, S=2048, D=128, causal.  Prints one JSON
 line: TFLOP/s from FLOPs = 10*B*H*S^2*D*0.5, ms per backward, % of fp16 dense
 MFMA peak, the main kernel's roofline (HIP events recorded by the library at
@@ -91,6 +91,19 @@ class Hip:
         assert self.lib.hipDeviceSynchronize() == 0
 
 
+def load_traffic(config):
+    """HBM bytes per launch of the main kernel, measured with rocprofv3
+    FETCH_SIZE / WRITE_SIZE and scaled by a copy kernel of known size
+    (profiles/traffic_bwd_fused_kernel.json, written from those runs)."""
+    path = os.path.join(ROOT, "profiles", "traffic_bwd_fused_kernel.json")
+    try:
+        with open(path) as fh:
+            entry = json.load(fh).get(config)
+    except (OSError, ValueError):
+        return None
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
 def cpu_baseline(cfg, budget_s):
     """Time the CPU oracle's backward (fp32, threaded) on a bounded sample of
     the same workload: whole (batch, kv-head) groups of the config, repeated
@@ -132,6 +145,9 @@ def main():
     ap.add_argument("--deterministic", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU oracle work for cpu_baseline (0 disables)")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="after timing, run a plain device copy of this many MiB "
+                         "(reference kernel for rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -181,22 +197,25 @@ def main():
     f = flops(B, Hq, S, D, causal)
     tflops = f / (ms * 1e-3) / 1e12
 
-    # ---- per-stage durations from the library's stage events ----
+    # ---- per-kernel durations from the library's stage events (null stream) ----
     evs = [hip.event() for _ in range(4)]
     p.reserved_i32[15] = STAGE_TAG
     for i, e in enumerate(evs):
         p.reserved_ptr[4 + i] = e.value
-    stage = [0.0, 0.0, 0.0]
+    stage = [0.0, 0.0]
     for _ in range(args.steps):
         step()
         hip.sync()
-        for i in range(3):
+        for i in range(2):
             stage[i] += hip.elapsed_ms(evs[i], evs[i + 1])
     p.reserved_i32[15] = 0
     stage = [s / args.steps for s in stage]
-    main_ms = stage[1]
+    pre_ms, main_ms = stage
     rows = B * Hq * S
-    pre_bytes = rows * D * 2 * 2 + rows * 4 * 3 + rows * D * 4  # O, dO, LSE in; delta, lse2 out; dQ acc clear
+    # preprocess algorithmic bytes: read O, dO (fp16) and LSE; write delta, lse2
+    pre_bytes = rows * D * 2 * 2 + rows * 4 * 3
+    main_tflops = f / (main_ms * 1e-3) / 1e12
+    traffic = load_traffic(args.config)
     result = {
         "metric": METRIC,
         "value": round(tflops, 3),
@@ -217,18 +236,26 @@ def main():
                    "flops_per_bwd": f},
         "pct_fp16_peak": round(100.0 * tflops / FP16_PEAK_TFLOPS, 3),
         "wall_s_timed": round(wall, 4),
-        "stages_ms": {"preprocess": round(stage[0], 5), "main": round(stage[1], 5),
-                      "dq_finalize": round(stage[2], 5)},
-        "roofline": {"kernel": "bwd_main_kernel", "bound": "mfma",
-                     "achieved": round(f / (main_ms * 1e-3) / 1e12, 3),
+        "kernels_ms": {"preprocess_kernel": round(pre_ms, 5), "bwd_fused_kernel": round(main_ms, 5)},
+        "roofline": {"kernel": "bwd_fused_kernel", "bound": "mfma",
+                     "achieved": round(main_tflops, 3),
                      "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(f / (main_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 5),
-                     "traffic": None},
-        "preprocess_roofline": {"bound": "hbm",
-                                "achieved": round(pre_bytes / (stage[0] * 1e-3) / 1e9, 1),
+                     "frac": round(main_tflops / FP16_PEAK_TFLOPS, 5),
+                     "traffic": traffic},
+        "preprocess_roofline": {"kernel": "preprocess_kernel", "bound": "hbm",
+                                "achieved": round(pre_bytes / (pre_ms * 1e-3) / 1e9, 1),
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                "frac": round(pre_bytes / (stage[0] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+                                "frac": round(pre_bytes / (pre_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
     }
+    if args.calib_copy_mb > 0:
+        # plain copy kernel of known size, for scaling rocprofv3 FETCH/WRITE_SIZE
+        n = args.calib_copy_mb * (1 << 20) // 4
+        x = torch.ones(n, dtype=torch.float32, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        result["calib_copy_bytes"] = n * 4
     if args.cpu_budget > 0:
         result["cpu_baseline"] = cpu_baseline(CONFIGS[args.config], args.cpu_budget)
     print(json.dumps(result), flush=True)

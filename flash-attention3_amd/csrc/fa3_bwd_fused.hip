@@ -49,8 +49,13 @@ struct FusedArgs {
     int heads_q;
     int heads_kv;
     int batch;
-    int n_kv_jobs;
-    int n_q_jobs;
+    // job map: n_groups (batch, kv head) groups of jobs_per_group jobs; with
+    // xcd_parts > 0 each group is split into xcd_parts interleaved parts of
+    // part_len jobs and whole parts are pinned to one XCD.
+    int n_groups;
+    int jobs_per_group;
+    int xcd_parts;
+    int part_len;
     float scale_log2;
     float scale;
 };
@@ -121,7 +126,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // dKV role
 // ----------------------------------------------------------------------------
 template <int D, bool kCausal>
-__device__ void dkv_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
+__device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem) {
     using C = Cfg<D>;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -131,9 +136,6 @@ __device__ void dkv_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
 
     const int S = a.seqlen;
     const int QT = S / 64;
-    const int kv_total = a.batch * a.heads_kv;
-    const int kt = job / kv_total;   // longest (causal) first
-    const int bkv = job % kv_total;
     const int group = a.heads_q / a.heads_kv;
     const int b = bkv / a.heads_kv;
     const int hkv = bkv % a.heads_kv;
@@ -321,7 +323,7 @@ __device__ void dkv_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
 // dQ role
 // ----------------------------------------------------------------------------
 template <int D, bool kCausal>
-__device__ void dq_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
+__device__ void dq_role(const FusedArgs& a, int bhq, int qt, FA3_LDS char* smem) {
     using C = Cfg<D>;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -331,9 +333,6 @@ __device__ void dq_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
 
     const int S = a.seqlen;
     const int QT = S / 64;
-    const int q_total = a.batch * a.heads_q;
-    const int qt = QT - 1 - job / q_total;  // longest (causal) first
-    const int bhq = job % q_total;
     const int group = a.heads_q / a.heads_kv;
     const int b = bhq / a.heads_q;
     const int bkv = b * a.heads_kv + (bhq % a.heads_q) / group;
@@ -465,30 +464,45 @@ __device__ void dq_role(const FusedArgs& a, int job, FA3_LDS char* smem) {
     }
 }
 
-// Grid: the two roles interleaved, each in longest-first order, so the
-// dispatcher starts the longest jobs first.
+// Job map.  Jobs are grouped by (batch, kv head) -- a group's dKV jobs and
+// the dQ jobs of its query heads touch only that head's Q, dO, K, V.  Within
+// a group, position p = (level L, slot r) with G + 1 slots per level: slot 0
+// is the dKV job of key tile L, slot r > 0 the dQ job of query head r - 1 at
+// query tile QT - 1 - L, so the dispatch order is longest first (causal).
+// The hardware deals consecutive workgroup ids round-robin to the 8 XCDs;
+// when the shape allows, block id -> (xcd, position) is arranged so that each
+// XCD runs whole parts of groups, keeping a head's tiles in one L2.
 template <int D, bool kCausal>
 __global__ __launch_bounds__(256, 1) void bwd_fused_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
     const int id = blockIdx.x;
-    const int both = a.n_kv_jobs < a.n_q_jobs ? a.n_kv_jobs : a.n_q_jobs;
-    bool kv;
-    int job;
-    if (id < 2 * both) {
-        kv = (id & 1) == 0;
-        job = id >> 1;
+    int g, pos;
+    if (a.xcd_parts > 0) {
+        const int xcd = id & 7;
+        const int n = id >> 3;
+        const int v = xcd + 8 * (n / a.part_len);  // virtual group = (group, part)
+        g = v / a.xcd_parts;
+        pos = v % a.xcd_parts + a.xcd_parts * (n % a.part_len);
     } else {
-        kv = a.n_kv_jobs > a.n_q_jobs;
-        job = both + (id - 2 * both);
+        g = id / a.jobs_per_group;
+        pos = id % a.jobs_per_group;
     }
-    if (kv) dkv_role<D, kCausal>(a, job, smem);
-    else dq_role<D, kCausal>(a, job, smem);
+    const int group = a.heads_q / a.heads_kv;
+    const int QT = a.seqlen / 64;
+    const int level = pos / (group + 1);
+    const int slot = pos % (group + 1);
+    if (slot == 0) {
+        dkv_role<D, kCausal>(a, g, level, smem);
+    } else {
+        const int b = g / a.heads_kv, hkv = g % a.heads_kv;
+        dq_role<D, kCausal>(a, b * a.heads_q + hkv * group + slot - 1, QT - 1 - level, smem);
+    }
 }
 
 template <int D>
 void launch_d(const FusedArgs& a, bool causal) {
-    const dim3 grid(a.n_kv_jobs + a.n_q_jobs);
+    const dim3 grid(a.n_groups * a.jobs_per_group);
     if (causal) hipLaunchKernelGGL((bwd_fused_kernel<D, true>), grid, dim3(256), 0, 0, a);
     else hipLaunchKernelGGL((bwd_fused_kernel<D, false>), grid, dim3(256), 0, 0, a);
 }
@@ -524,8 +538,16 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     a.heads_q = p.heads_q;
     a.heads_kv = p.heads_kv;
     a.batch = p.batch;
-    a.n_kv_jobs = (p.seqlen / kTileN) * p.batch * p.heads_kv;
-    a.n_q_jobs = (p.seqlen / kTileM) * p.batch * p.heads_q;
+    a.n_groups = p.batch * p.heads_kv;
+    a.jobs_per_group = (p.seqlen / kTileN) * (1 + p.heads_q / p.heads_kv);
+    {
+        int gcd8 = 8;
+        while (a.n_groups % gcd8 != 0) gcd8 >>= 1;
+        const int parts = 8 / gcd8;  // smallest split with n_groups * parts % 8 == 0
+        const bool fits = a.jobs_per_group % parts == 0;
+        a.xcd_parts = fits ? parts : 0;
+        a.part_len = fits ? a.jobs_per_group / parts : 0;
+    }
     a.scale_log2 = p.scale * kLog2e;
     a.scale = p.scale;
     if (p.head_dim == 128) launch_d<128>(a, p.causal);
