@@ -19,16 +19,24 @@
 //
 // The softmax scale is folded out of dS and applied once to dK and dQ.
 //
-// Wave layout: 4 waves, wave w = (w & 1, w >> 1) = (key half, query half) in
-// the dKV role and (query half, key half) in the dQ role; each wave works on
-// a 32 x 32 score block with v_mfma_f32_32x32x16_f16.  The two waves that
-// share an output block add their partials through LDS once at the end.
-//
-// Pipeline: streamed tiles live in four LDS buffers filled by direct-to-LDS
-// loads (global_load_lds_dwordx4) issued three tiles ahead; iteration `it`
-// runs the softmax of tile it (VALU) beside S/dP of tile it+1 (MFMA), then
-// the dV/dK (or dQ) MFMAs of tile it.  Waits use explicit vmcnt values so the
-// loads of the following tile stay in flight across the barrier.
+// Each workgroup has 8 waves, two per SIMD, so one wave's MFMAs overlap the
+// other's softmax, LDS traffic and waits.  A pipeline step has two phases:
+//   phase 1: the 64 x 64 score and dP tiles in 16 x 16 blocks
+//            (v_mfma_f32_16x16x32_f16); each wave owns 16 x 32 of them and
+//            turns them into P / dS (fp16), which it writes to LDS;
+//   phase 2: the output products with v_mfma_f32_32x32x16_f16; each wave owns
+//            a 32-wide slice of D (and, where there are more waves than
+//            slices, part of the contraction, added through LDS at the end),
+//            reading P / dS from LDS; its other operand (the streamed tile,
+//            transposed by ds_read_b64_tr_b16) is read one step earlier, in
+//            phase 1 of that tile, and carried in registers.
+// Step j runs phase 1 of tile j + 1 and phase 2 of tile j, so P / dS are
+// double-buffered and one barrier per step suffices.  Every global read of
+// the loop is a direct-to-LDS load (global_load_lds) into one of three
+// stages, issued two steps ahead: a stage holds a streamed tile pair and, in
+// the dKV role, its 64 lse2 / delta values.  The issue pattern is the same
+// every step (a finished stream re-loads its last tile into a free stage), so
+// every wait is a constant count.
 #include "fa3_bwd_device.h"
 #include "fa3_bwd_internal.h"
 
@@ -41,7 +49,7 @@ struct FusedArgs {
     const _Float16* v;
     const _Float16* dout;
     const float* lse2;   // [B*Hq*S]
-    const float* delta;  // [B*Hq*S]
+    const float* ndelta; // [B*Hq*S], -delta
     _Float16* dq;
     _Float16* dk;
     _Float16* dv;
@@ -60,43 +68,71 @@ struct FusedArgs {
     float scale;
 };
 
-constexpr int kNBuf = 4;
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kStages = 3;
 
 template <int D>
 struct Cfg {
-    static constexpr int kTileBytes = 64 * D * 2;          // one [64][D] fp16 tile
-    static constexpr int kKSteps = D / 16;                 // MFMA k-steps over D
-    static constexpr int kMB = D / 32;                     // 32-row blocks of D
-    static constexpr int kChunks = D / 8;                  // 16-byte chunks per row
-    static constexpr int kLoadsPerWave = kTileBytes / 1024 / 4;
-    // dKV role buffer: Q tile, dO tile, lse2[64], delta[64]
-    static constexpr int kKvRows = 2 * kTileBytes;
-    static constexpr int kKvBuf = kKvRows + 2 * 64 * 4;
-    // dQ role buffer: K tile, V tile
-    static constexpr int kQBuf = 2 * kTileBytes;
-    static constexpr int kBytes = kNBuf * (kKvBuf > kQBuf ? kKvBuf : kQBuf);
-    // final cross-wave exchange: 2 waves x kMB x 16 x 64 floats
-    static_assert(2 * kMB * 16 * 64 * 4 <= kBytes, "exchange fits in the buffers");
+    static constexpr int kTileBytes = 64 * D * 2;           // one [64][D] fp16 tile
+    static constexpr int kRowsBytes = 2 * 64 * 4;           // lse2[64], delta[64]
+    static constexpr int kStageBytes = 2 * kTileBytes + kRowsBytes;
+    static constexpr int kKs = D / 32;                      // 16x16x32 k-steps over D
+    static constexpr int kDB = D / 32;                      // 32-wide slices of D
+    static constexpr int kChunks = D / 8;                   // 16-byte chunks per row
+    static constexpr int kLoadsPerTile = kTileBytes / (kWaves * 1024);  // per lane
+    // direct-to-LDS loads per wave and stage: dKV Q, dO, rows; dQ K, V
+    static constexpr int kDmaKv = 2 * kLoadsPerTile + 1;
+    static constexpr int kDmaQ = 2 * kLoadsPerTile;
+    // phase-2 split: the dKV role has 2 * kDB (matrix, D-slice) pairs, the dQ
+    // role kDB D-slices; the 8 waves cover them with kSplitKv / kSplitQ waves
+    // each, splitting the 4 contraction steps of a tile between them.
+    static constexpr int kPairsKv = 2 * kDB;
+    static constexpr int kSplitKv = kWaves / kPairsKv;
+    static constexpr int kStepsKv = 4 / kSplitKv;
+    static constexpr int kSplitQ = kWaves / kDB;
+    static constexpr int kStepsQ = 4 / kSplitQ;
+    static constexpr int kPdsBytes = 64 * 64 * 2;           // one [64][64] fp16 tile
+    static constexpr int kPdsOff = kStages * kStageBytes;   // P / dS double buffer
+    static constexpr int kBytes = kPdsOff + 2 * 2 * kPdsBytes;
+    static_assert(kLoadsPerTile >= 1, "tile covers all waves");
+    static_assert(kStageBytes % 512 == 0 && kPdsOff % 512 == 0, "bank-aligned tiles");
+    static_assert(2 * kTileBytes <= 2 * 2 * kPdsBytes, "prologue staging fits the P / dS area");
+    static_assert(kBytes <= 160 * 1024, "LDS budget");
+    static_assert(kWaves * 2 * 16 * 64 * 4 <= kBytes, "epilogue exchange fits");
 };
 
-// s_waitcnt vmcnt(N) leaving the LDS and export counters alone.
+// s_waitcnt vmcnt(N) lgkmcnt(0): all but the last N vector-memory loads have
+// landed and this wave's LDS accesses are done.
 template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
+__device__ __forceinline__ void wait_vm_lgkm0() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier that the compiler may not move memory accesses across.
+__device__ __forceinline__ void barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ f32x4 mfma_16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // Direct-to-LDS copy of a row-major [64][D] fp16 tile into a swizzled LDS
 // tile.  Lane `lane` of wave `wave` moves the 16-byte chunk that belongs at
-// LDS byte blk * 1024 + lane * 16 (blk = wave * kLoadsPerWave + j); its
+// LDS byte blk * 1024 + lane * 16 (blk = wave * kLoadsPerTile + j); its
 // source byte offset within the global tile is precomputed once.
 template <int D>
-__device__ __forceinline__ void tile_load_offsets(uint32_t (&off)[Cfg<D>::kLoadsPerWave],
+__device__ __forceinline__ void tile_load_offsets(uint32_t (&off)[Cfg<D>::kLoadsPerTile],
                                                   int wave, int lane) {
     using C = Cfg<D>;
 #pragma unroll
-    for (int j = 0; j < C::kLoadsPerWave; ++j) {
-        const int id = (wave * C::kLoadsPerWave + j) * 64 + lane;  // physical chunk
+    for (int j = 0; j < C::kLoadsPerTile; ++j) {
+        const int id = (wave * C::kLoadsPerTile + j) * 64 + lane;  // physical chunk
         const int row = id / C::kChunks;
         const int phys = id % C::kChunks;
         int sw;
@@ -109,18 +145,59 @@ __device__ __forceinline__ void tile_load_offsets(uint32_t (&off)[Cfg<D>::kLoads
 
 template <int D>
 __device__ __forceinline__ void load_tile_async(FA3_LDS char* tile, const _Float16* src,
-                                                const uint32_t (&off)[Cfg<D>::kLoadsPerWave],
+                                                const uint32_t (&off)[Cfg<D>::kLoadsPerTile],
                                                 int wave) {
     using C = Cfg<D>;
 #pragma unroll
-    for (int j = 0; j < C::kLoadsPerWave; ++j) {
+    for (int j = 0; j < C::kLoadsPerTile; ++j) {
         __builtin_amdgcn_global_load_lds((const void*)((const char*)src + off[j]),
-                                         (FA3_LDS void*)(tile + (wave * C::kLoadsPerWave + j) * 1024),
+                                         (FA3_LDS void*)(tile + (wave * C::kLoadsPerTile + j) * 1024),
                                          16, 0, 0);
     }
 }
 
+// Direct-to-LDS copy of the lse2 and -delta values of 64 query rows starting
+// at row0 into rows[0..64) and rows[64..128): wave w moves 16 of them with
+// lanes 0..15 (one dword each), so every wave issues exactly one load.
+__device__ __forceinline__ void load_rows_async(FA3_LDS char* rows, const float* lse2,
+                                                const float* ndelta, size_t row0, int w, int lane) {
+    const float* src = (w < 4 ? lse2 : ndelta) + row0 + 16 * (w & 3) + lane;
+    FA3_LDS char* dst = rows + 256 * (w >> 2) + 64 * (w & 3);
+    if (lane < 16) __builtin_amdgcn_global_load_lds((const void*)src, (FA3_LDS void*)dst, 4, 0, 0);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// A operand (32 x 16: m = D column, k = tile row) of a phase-2 product, read
+// transposed from a swizzled [64][D] tile: lane l gets column 32 db + l % 32,
+// rows 16 ks + 8 (l / 32) + t, t = 0..7 (two reads of 4 rows).
+template <int D>
+__device__ __forceinline__ f16x8 tile_read_t(const FA3_LDS char* tile, int db, int ks, int lane) {
+    const int g = lane >> 4, r = lane & 15;
+    const int col = 32 * db + 16 * (g & 1) + 4 * (r & 3);
+    const int row = 16 * ks + 8 * (g >> 1) + (r >> 2);
+    const uint32_t lo = tile_off<D>(row, col >> 3) + (col & 7) * 2;
+    const uint32_t hi = tile_off<D>(row + 4, col >> 3) + (col & 7) * 2;
+    return concat4(lds_read_tr4(tile, lo), lds_read_tr4(tile, hi));
+}
+
+// 16-byte chunk of D that lane group g4 (= lane / 16) reads in k-step s of
+// a 16x16x32 MFMA operand taken from 16 consecutive rows of a [64][D] tile.
+// ds_read_b128 serves a wave in four groups of 16 lanes, lane l belonging to
+// group (l / 32, parity of bits 2..4 of l); with the tile swizzle of
+// tile_off<D> these orders give every group 16 distinct bank quads (the
+// order 4 s + g4 would put two lanes of a group on one quad).
+template <int D>
+__device__ __forceinline__ int p1_chunk(int s, int g4) {
+    if constexpr (D == 128) return s + 4 * g4;
+    else return s + 2 * (g4 >> 1) + 4 * (g4 & 1);
+}
+
+// Byte offset of the 8-byte group (row r, columns 4 q .. 4 q + 3) of a
+// swizzled [64][64] fp16 P / dS tile.
+__device__ __forceinline__ uint32_t pds_off4(int r, int q) {
+    return dst_off(r, q >> 1) + (q & 1) * 8;
+}
 
 // ----------------------------------------------------------------------------
 // dKV role
@@ -131,8 +208,17 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wk = w & 1, wq = w >> 1;
-    const int l32 = lane & 31, h = lane >> 5, g = lane >> 4, r16 = lane & 15;
+    const int l16 = lane & 15, g4 = lane >> 4, l32 = lane & 31, h = lane >> 5;
+    // phase 1: query rows 16 rs .. +16, keys 32 kh .. +32 (two 16-key blocks)
+    const int rs = w & 3, kh = w >> 2;
+    // phase 2: matrix (0: dV from dO and P, 1: dK from Q and dS), D slice db,
+    // contraction steps ks0 .. ks0 + kStepsKv of each tile
+    const int pair = w % C::kPairsKv;
+    const int mat = pair / C::kDB, db = pair % C::kDB;
+    const int part = w / C::kPairsKv;
+    const int ks0 = part * C::kStepsKv;
+    constexpr int kP2 = 2 * C::kStepsKv;  // phase-2 MFMAs per step
+    constexpr int kPer = 8 / kP2;         // softmax elements paired with each
 
     const int S = a.seqlen;
     const int QT = S / 64;
@@ -140,180 +226,262 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem
     const int b = bkv / a.heads_kv;
     const int hkv = bkv % a.heads_kv;
     const int kbase = kt * 64;
-
-    const _Float16* kp = a.k + ((size_t)bkv * S + kbase) * D;
-    const _Float16* vp = a.v + ((size_t)bkv * S + kbase) * D;
-    f16x8 kf[C::kKSteps], vf[C::kKSteps];
-#pragma unroll
-    for (int s = 0; s < C::kKSteps; ++s) {
-        kf[s] = *(const f16x8*)(kp + (32 * wk + l32) * D + 16 * s + 8 * h);
-        vf[s] = *(const f16x8*)(vp + (32 * wk + l32) * D + 16 * s + 8 * h);
-    }
-    f32x16 dkt[C::kMB], dvt[C::kMB];
-#pragma unroll
-    for (int mb = 0; mb < C::kMB; ++mb) {
-        dkt[mb] = f32x16{};
-        dvt[mb] = f32x16{};
-    }
-
     const int qt0 = kCausal ? kt : 0;
-    const int per_head = QT - qt0;
-    const int n_it = group * per_head;
-    uint32_t ld_off[C::kLoadsPerWave];
+    const int n_it = group * (QT - qt0);
+
+    uint32_t ld_off[C::kLoadsPerTile];
     tile_load_offsets<D>(ld_off, w, lane);
 
-    // Tiles are issued in order; (issue_bhq, issue_qt) is the next one.
-    int issue_bhq = b * a.heads_q + hkv * group;
-    int issue_qt = qt0;
-    auto issue_next = [&](int slot) {
-        const size_t row0 = (size_t)issue_bhq * S + issue_qt * 64;
-        FA3_LDS char* nb = smem + slot * C::kKvBuf;
-        load_tile_async<D>(nb, a.q + row0 * D, ld_off, w);
-        load_tile_async<D>(nb + C::kTileBytes, a.dout + row0 * D, ld_off, w);
-        if (w == 0) {
-            __builtin_amdgcn_global_load_lds((const void*)(a.lse2 + row0 + lane),
-                                             (FA3_LDS void*)(nb + C::kKvRows), 4, 0, 0);
-        } else if (w == 1) {
-            __builtin_amdgcn_global_load_lds((const void*)(a.delta + row0 + lane),
-                                             (FA3_LDS void*)(nb + C::kKvRows + 256), 4, 0, 0);
-        }
-        if (++issue_qt == QT) {
-            issue_qt = qt0;
-            ++issue_bhq;
-        }
-    };
-    // vmcnt allowing `tiles` tiles of this wave's loads to stay in flight
-    auto wait_tiles = [&](int tiles) {
-        if (w < 2) {
-            if (tiles >= 2) wait_vmcnt<2 * (2 * C::kLoadsPerWave + 1)>();
-            else if (tiles == 1) wait_vmcnt<2 * C::kLoadsPerWave + 1>();
-            else wait_vmcnt<0>();
-        } else {
-            if (tiles >= 2) wait_vmcnt<2 * (2 * C::kLoadsPerWave)>();
-            else if (tiles == 1) wait_vmcnt<2 * C::kLoadsPerWave>();
-            else wait_vmcnt<0>();
-        }
-    };
-
-    // S = Q K^T, dP = dO V^T (wave: q rows 32wq.., keys 32wk..)
-    auto stage_a = [&](FA3_LDS char* buf, f32x16& sacc, f32x16& pacc) {
-        sacc = f32x16{};
-        pacc = f32x16{};
-#pragma unroll
-        for (int s = 0; s < C::kKSteps; ++s) {
-            const uint32_t off = tile_off<D>(32 * wq + l32, 2 * s + h);
-            sacc = mfma_32x32x16(lds_read_b128(buf, off), kf[s], sacc);
-            pacc = mfma_32x32x16(lds_read_b128(buf + C::kTileBytes, off), vf[s], pacc);
-        }
-    };
-    // P and dS; lane holds key 32wk + l32, q = 32wq + 8(i/4) + 4h + i%4.
-    auto stage_b = [&](auto masked, const f32x16& sacc, const f32x16& pacc,
-                       const FA3_LDS char* buf, f16x8 (&pb)[2], f16x8 (&dsb)[2]) {
-        const FA3_LDS float* rows = (const FA3_LDS float*)(buf + C::kKvRows);
-#pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) {
-            const f32x4 l2 = *(const FA3_LDS f32x4*)(rows + 32 * wq + 8 * a4 + 4 * h);
-            const f32x4 dl = *(const FA3_LDS f32x4*)(rows + 64 + 32 * wq + 8 * a4 + 4 * h);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int i = 4 * a4 + e;
-                float p = fast_exp2(sacc[i] * a.scale_log2 - l2[e]);
-                if constexpr (decltype(masked)::value) {
-                    if (32 * wk + l32 > 32 * wq + 8 * a4 + 4 * h + e) p = 0.f;
-                }
-                pb[i >> 3][i & 7] = (_Float16)p;
-                dsb[i >> 3][i & 7] = (_Float16)(p * (pacc[i] - dl[e]));
+    // Cursor of the next query tile to load; a finished stream keeps
+    // re-loading its last tile (into a stage nobody reads), so every step
+    // issues the same loads.
+    int ld_bhq = b * a.heads_q + hkv * group, ld_qt = qt0, ld_left = n_it;
+    auto issue = [&](FA3_LDS char* st) {
+        const size_t row0 = (size_t)ld_bhq * S + ld_qt * 64;
+        load_tile_async<D>(st, a.q + row0 * D, ld_off, w);
+        load_tile_async<D>(st + C::kTileBytes, a.dout + row0 * D, ld_off, w);
+        load_rows_async(st + 2 * C::kTileBytes, a.lse2, a.ndelta, row0, w, lane);
+        if (--ld_left > 0) {
+            if (++ld_qt == QT) {
+                ld_qt = qt0;
+                ++ld_bhq;
             }
         }
     };
-    // dV^T += dO^T P, dK^T += Q^T dS; A operands by transposed reads with
-    // q = 16ks + 8u + 4h + j matching the C-register order of P / dS.
-    auto stage_c = [&](FA3_LDS char* buf, const f16x8 (&pb)[2], const f16x8 (&dsb)[2]) {
+    // query tile of the next softmax: the causal diagonal needs the mask
+    int sm_qt = qt0;
+    auto next_masked = [&]() {
+        const bool m = kCausal && sm_qt == kt;
+        if (++sm_qt == QT) sm_qt = qt0;
+        return m;
+    };
+
+    // B operands: key 32 kh + 16 kb + l16, D chunk p1_chunk(s, g4)
+    f16x8 kf[2][C::kKs], vf[2][C::kKs];
+    f32x16 acc[2];
+    acc[0] = f32x16{};
+    acc[1] = f32x16{};
+    // S and dP - delta of rows 16 rs + 4 g4 + i, keys 32 kh + 16 kb + l16
+    f32x4 sacc[2], pacc[2];
+
+    // phase-1 A operands (Q, dO rows 16 rs + l16) and lse2 / -delta of the
+    // lane's rows, from the stage of one tile
+    auto p1_read = [&](const FA3_LDS char* st, f16x8 (&aq)[C::kKs], f16x8 (&ad)[C::kKs],
+                       f32x4& l2, f32x4& ndl) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int s = 0; s < C::kKs; ++s) {
+            const uint32_t off = tile_off<D>(16 * rs + l16, p1_chunk<D>(s, g4));
+            aq[s] = lds_read_b128(st, off);
+            ad[s] = lds_read_b128(st + C::kTileBytes, off);
+        }
+        const FA3_LDS char* r = st + 2 * C::kTileBytes + (16 * rs + 4 * g4) * 4;
+        l2 = *(const FA3_LDS f32x4*)r;
+        ndl = *(const FA3_LDS f32x4*)(r + 256);
+    };
+    // S = Q K^T and dP - delta = dO V^T - delta (the accumulator starts at -delta)
+    auto p1_mfma = [&](const f16x8 (&aq)[C::kKs], const f16x8 (&ad)[C::kKs], const f32x4& ndl) {
 #pragma unroll
-            for (int mb = 0; mb < C::kMB; ++mb) {
-                f16x4 ao[2], aq[2];
+        for (int s = 0; s < C::kKs; ++s) {
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const int row = 32 * wq + 16 * ks + 8 * u + 4 * h + (r16 >> 2);
-                    const int col = 32 * mb + 16 * (g & 1) + 4 * (r16 & 3);
-                    const uint32_t off = tile_off<D>(row, col >> 3) + (col & 7) * 2;
-                    ao[u] = lds_read_tr4(buf + C::kTileBytes, off);
-                    aq[u] = lds_read_tr4(buf, off);
-                }
-                dvt[mb] = mfma_32x32x16(concat4(ao[0], ao[1]), pb[ks], dvt[mb]);
-                dkt[mb] = mfma_32x32x16(concat4(aq[0], aq[1]), dsb[ks], dkt[mb]);
+            for (int kb = 0; kb < 2; ++kb) {
+                sacc[kb] = mfma_16x16x32(aq[s], kf[kb][s], s == 0 ? f32x4{} : sacc[kb]);
+                pacc[kb] = mfma_16x16x32(ad[s], vf[kb][s], s == 0 ? ndl : pacc[kb]);
             }
         }
     };
-    // One pipeline step on tile `it`: softmax of it, S/dP of it+1, dV/dK of
-    // it.  The last step computes S/dP on a stale buffer and drops them, so
-    // every step has the same straight-line body.
-    auto step = [&](auto masked, int it, f32x16& sacc, f32x16& pacc) {
-        const int slot = it & (kNBuf - 1);
-        if (it + 1 < n_it) {
-            wait_tiles(it + 2 < n_it ? 1 : 0);  // tile it+1 landed everywhere
-            __builtin_amdgcn_s_barrier();        // and tile it-1's buffer is free
-            if (it + 3 < n_it) issue_next((it + 3) & (kNBuf - 1));
+    // phase-2 A operands of the tile in `st`: dO^T (dV waves) or Q^T (dK waves)
+    auto read_xt = [&](const FA3_LDS char* st, f16x8 (&xt)[C::kStepsKv]) {
+        const FA3_LDS char* x = st + (mat == 0 ? C::kTileBytes : 0);
+#pragma unroll
+        for (int j = 0; j < C::kStepsKv; ++j) xt[j] = tile_read_t<D>(x, db, ks0 + j, lane);
+    };
+    // phase-2 B operands: P (dV waves) or dS (dK waves), keys 32 kb + l32
+    auto read_pds = [&](const FA3_LDS char* pds, f16x8 (&bp)[C::kStepsKv][2]) {
+        const FA3_LDS char* pm = pds + mat * C::kPdsBytes;
+#pragma unroll
+        for (int j = 0; j < C::kStepsKv; ++j)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+                bp[j][kb] = lds_read_b128(pm, dst_off(32 * kb + l32, 2 * (ks0 + j) + h));
+    };
+    // softmax element e = 4 kb + i: P = exp2(S c - lse2), dS = P (dP - delta)
+    auto sm_elem = [&](int e, const f32x4& l2, float (&p)[8], float (&ds)[8]) {
+        const int kb = e >> 2, i = e & 3;
+        p[e] = fast_exp2(sacc[kb][i] * a.scale_log2 - l2[i]);
+        ds[e] = p[e] * pacc[kb][i];
+    };
+    // causal mask (diagonal tile only), fp16 P / dS written transposed
+    // ([key][row]) into the P / dS buffer
+    auto store_pds = [&](bool masked, float (&p)[8], float (&ds)[8], FA3_LDS char* pds) {
+        if (masked) {
+            __asm__ volatile("" ::: "memory");  // keep this a branch: off the diagonal it is skipped
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                if (32 * kh + 16 * (e >> 2) + l16 > 16 * rs + 4 * g4 + (e & 3)) {
+                    p[e] = 0.f;
+                    ds[e] = 0.f;
+                }
+            }
         }
-        __builtin_amdgcn_sched_barrier(0);
-        f16x8 pb[2], dsb[2];
-        FA3_LDS char* buf = smem + slot * C::kKvBuf;
-        stage_b(masked, sacc, pacc, buf, pb, dsb);
-        stage_a(smem + ((slot + 1) & (kNBuf - 1)) * C::kKvBuf, sacc, pacc);
-        stage_c(buf, pb, dsb);
-        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            f16x4 pv, dv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pv[i] = (_Float16)p[4 * kb + i];
+                dv[i] = (_Float16)ds[4 * kb + i];
+            }
+            const uint32_t off = pds_off4(32 * kh + 16 * kb + l16, 4 * rs + g4);
+            lds_write_b64(pds, off, pv);
+            lds_write_b64(pds + C::kPdsBytes, off, dv);
+        }
     };
 
-    // prologue: up to three tiles in flight, S/dP of tile 0
-    const int pre = n_it < 3 ? n_it : 3;
-    for (int i = 0; i < pre; ++i) issue_next(i);
-    wait_tiles(pre - 1);
-    __builtin_amdgcn_s_barrier();
-    f32x16 sacc, pacc;
-    stage_a(smem, sacc, pacc);
+    // The LDS regions a step touches are passed as restrict pointers, so the
+    // compiler can tell that its reads do not depend on the direct-to-LDS
+    // loads into other regions and adds no wait for those loads.
+    f16x8 xa[C::kStepsKv], xb[C::kStepsKv];
+    auto prologue = [&](FA3_LDS char* __restrict__ s0, FA3_LDS char* __restrict__ s1,
+                        FA3_LDS char* __restrict__ s2, FA3_LDS char* __restrict__ pa) {
+        // this key tile's K and V are staged in the P / dS area
+        const size_t k0 = (size_t)bkv * S + kbase;
+        load_tile_async<D>(pa, a.k + k0 * D, ld_off, w);
+        load_tile_async<D>(pa + C::kTileBytes, a.v + k0 * D, ld_off, w);
+        issue(s0);
+        issue(s1);
+        issue(s2);
+        wait_vm_lgkm0<2 * C::kDmaKv>();
+        barrier();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int s = 0; s < C::kKs; ++s) {
+                const uint32_t off = tile_off<D>(32 * kh + 16 * kb + l16, p1_chunk<D>(s, g4));
+                kf[kb][s] = lds_read_b128(pa, off);
+                vf[kb][s] = lds_read_b128(pa + C::kTileBytes, off);
+            }
+        f16x8 aq[C::kKs], ad[C::kKs];
+        f32x4 l2, ndl;
+        p1_read(s0, aq, ad, l2, ndl);
+        p1_mfma(aq, ad, ndl);
+        read_xt(s0, xa);
+        float p[8], ds[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm_elem(e, l2, p, ds);
+        wait_vm_lgkm0<2 * C::kDmaKv>();  // K / V reads done before P / dS overwrite them
+        barrier();
+        store_pds(next_masked(), p, ds, pa);
+    };
+    // Step j: tile j + 1 landed everywhere and P / dS of tile j are written;
+    // the stage of tile j (read during step j - 1) is free for tile j + 3.
+    //   A: phase-1 operands of tile j + 1;
+    //   B: its S / dP MFMAs, beside the reads of P / dS (j) and of the
+    //      transposed operands of tile j + 1 (used in step j + 1);
+    //   C: the phase-2 MFMAs of tile j, each with a slice of the softmax of
+    //      tile j + 1, so the MFMA pipe has work while the VALU runs;
+    //   D: mask, pack and write P / dS (j + 1).
+    auto step = [&](FA3_LDS char* __restrict__ ld, const FA3_LDS char* __restrict__ s1,
+                    const FA3_LDS char* __restrict__ prd, FA3_LDS char* __restrict__ pwr,
+                    const f16x8 (&xcur)[C::kStepsKv], f16x8 (&xnext)[C::kStepsKv]) {
+        wait_vm_lgkm0<C::kDmaKv>();
+        barrier();
+        issue(ld);
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 aq[C::kKs], ad[C::kKs];
+        f32x4 l2, ndl;
+        p1_read(s1, aq, ad, l2, ndl);
+        f16x8 bp[C::kStepsKv][2];
+        read_pds(prd, bp);
+        p1_mfma(aq, ad, ndl);
+        read_xt(s1, xnext);
+        __builtin_amdgcn_sched_barrier(0);
+        float p[8], ds[8];
+#pragma unroll
+        for (int m = 0; m < kP2; ++m) {
+            acc[m & 1] = mfma_32x32x16(xcur[m >> 1], bp[m >> 1][m & 1], acc[m & 1]);
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) sm_elem(m * kPer + e, l2, p, ds);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        store_pds(next_masked(), p, ds, pwr);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto last = [&](const f16x8 (&xcur)[C::kStepsKv], const FA3_LDS char* __restrict__ prd) {
+        wait_vm_lgkm0<C::kDmaKv>();
+        barrier();
+        f16x8 bp[C::kStepsKv][2];
+        read_pds(prd, bp);
+#pragma unroll
+        for (int m = 0; m < kP2; ++m)
+            acc[m & 1] = mfma_32x32x16(xcur[m >> 1], bp[m >> 1][m & 1], acc[m & 1]);
+    };
 
-    // The causal diagonal is the first query tile of every head in the group.
-    int it = 0;
-    for (int gi = 0; gi < group; ++gi) {
-        if (kCausal) step(std::true_type{}, it, sacc, pacc);
-        else step(std::false_type{}, it, sacc, pacc);
-        ++it;
-        for (int j = 1; j < per_head; ++j, ++it) step(std::false_type{}, it, sacc, pacc);
+    FA3_LDS char* st_ld = smem;                     // stage of tile j (refilled in step j)
+    FA3_LDS char* st_1 = smem + C::kStageBytes;      // stage of tile j + 1
+    FA3_LDS char* st_2 = smem + 2 * C::kStageBytes;  // stage of tile j + 2
+    auto rotate = [&]() {
+        FA3_LDS char* t = st_ld;
+        st_ld = st_1;
+        st_1 = st_2;
+        st_2 = t;
+    };
+    FA3_LDS char* pds0 = smem + C::kPdsOff;
+    FA3_LDS char* pds1 = pds0 + 2 * C::kPdsBytes;
+
+    prologue(st_ld, st_1, st_2, pds0);
+    int j = 0;
+    for (; j + 2 < n_it; j += 2) {  // two steps per trip: xa / xb alternate
+        step(st_ld, st_1, pds0, pds1, xa, xb);
+        rotate();
+        step(st_ld, st_1, pds1, pds0, xb, xa);
+        rotate();
+    }
+    if (j + 1 < n_it) {
+        step(st_ld, st_1, pds0, pds1, xa, xb);
+        last(xb, pds1);
+    } else {
+        last(xa, pds0);
     }
 
-    // Combine the two query-half partials; lane: key 32wk + l32,
-    // d = 32mb + 8(i/4) + 4h + i%4.
-    FA3_LDS float* xch = (FA3_LDS float*)smem + wk * (C::kMB * 16 * 64);
-    _Float16* dkp = a.dk + ((size_t)bkv * S + kbase + 32 * wk + l32) * D;
-    _Float16* dvp = a.dv + ((size_t)bkv * S + kbase + 32 * wk + l32) * D;
+    // Epilogue: add the contraction-split partials through LDS in a fixed
+    // order (head dim 64), then store; lane: key 32 kb + l32,
+    // d = 32 db + 8 (i / 4) + 4 h + i % 4.
+    wait_vm_lgkm0<0>();
+    barrier();
+    if constexpr (C::kSplitKv > 1) {
+        FA3_LDS float* xch = (FA3_LDS float*)smem + w * (2 * 16 * 64);
+        if (part > 0) {
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-        f32x16* acc = pass == 0 ? dvt : dkt;
-        const float mul = pass == 0 ? 1.f : a.scale;
-        _Float16* outp = pass == 0 ? dvp : dkp;
-        __syncthreads();
-        if (wq == 1) {
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int mb = 0; mb < C::kMB; ++mb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) xch[(mb * 16 + i) * 64 + lane] = acc[mb][i];
+                for (int i = 0; i < 16; ++i) xch[(kb * 16 + i) * 64 + lane] = acc[kb][i];
         }
-        __syncthreads();
-        if (wq == 0) {
+        wait_vm_lgkm0<0>();
+        barrier();
+        if (part == 0) {
 #pragma unroll
-            for (int mb = 0; mb < C::kMB; ++mb) {
+            for (int p = 1; p < C::kSplitKv; ++p) {
+                const FA3_LDS float* src =
+                    (const FA3_LDS float*)smem + (w + p * C::kPairsKv) * (2 * 16 * 64);
 #pragma unroll
-                for (int a4 = 0; a4 < 4; ++a4) {
-                    f16x4 o;
+                for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int i = 4 * a4 + e;
-                        o[e] = (_Float16)((acc[mb][i] + xch[(mb * 16 + i) * 64 + lane]) * mul);
-                    }
-                    *(f16x4*)(outp + 32 * mb + 8 * a4 + 4 * h) = o;
-                }
+                    for (int i = 0; i < 16; ++i) acc[kb][i] += src[(kb * 16 + i) * 64 + lane];
+            }
+        }
+    }
+    if (part == 0) {
+        const float mul = mat == 0 ? 1.f : a.scale;
+        _Float16* outp =
+            (mat == 0 ? a.dv : a.dk) + ((size_t)bkv * S + kbase) * D + 32 * db + 4 * h;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int a4 = 0; a4 < 4; ++a4) {
+                f16x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[kb][4 * a4 + e] * mul);
+                *(f16x4*)(outp + (size_t)(32 * kb + l32) * D + 8 * a4) = o;
             }
         }
     }
@@ -328,137 +496,234 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, FA3_LDS char* smem)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wq = w & 1, wk = w >> 1;
-    const int l32 = lane & 31, h = lane >> 5, g = lane >> 4, r16 = lane & 15;
+    const int l16 = lane & 15, g4 = lane >> 4, l32 = lane & 31, h = lane >> 5;
+    // phase 1: keys 16 kq .. +16, query rows 32 rh .. +32 (two 16-row blocks)
+    const int kq = w & 3, rh = w >> 2;
+    // phase 2: D slice db, contraction steps ks0 .. ks0 + kStepsQ of each tile
+    const int db = w % C::kDB;
+    const int part = w / C::kDB;
+    const int ks0 = part * C::kStepsQ;
+    constexpr int kP2 = 2 * C::kStepsQ;
+    constexpr int kPer = 8 / kP2;
 
     const int S = a.seqlen;
     const int QT = S / 64;
     const int group = a.heads_q / a.heads_kv;
     const int b = bhq / a.heads_q;
     const int bkv = b * a.heads_kv + (bhq % a.heads_q) / group;
-    const int qbase = qt * 64;
-    const size_t row = (size_t)bhq * S + qbase + 32 * wq + l32;
-
-    // B operands of S^T = K Q^T and dP^T = V dO^T: q = row, d = 16s + 8h + t
-    f16x8 qf[C::kKSteps], df[C::kKSteps];
-#pragma unroll
-    for (int s = 0; s < C::kKSteps; ++s) {
-        qf[s] = *(const f16x8*)(a.q + row * D + 16 * s + 8 * h);
-        df[s] = *(const f16x8*)(a.dout + row * D + 16 * s + 8 * h);
-    }
-    const float l2 = a.lse2[row];
-    const float delta_row = a.delta[row];
-
-    f32x16 dqt[C::kMB];
-#pragma unroll
-    for (int mb = 0; mb < C::kMB; ++mb) dqt[mb] = f32x16{};
-
+    const size_t row0 = (size_t)bhq * S + qt * 64;
     const int n_kt = kCausal ? qt + 1 : QT;
+
+    uint32_t ld_off[C::kLoadsPerTile];
+    tile_load_offsets<D>(ld_off, w, lane);
     const _Float16* kh = a.k + (size_t)bkv * S * D;
     const _Float16* vh = a.v + (size_t)bkv * S * D;
-    uint32_t ld_off[C::kLoadsPerWave];
-    tile_load_offsets<D>(ld_off, w, lane);
-    int issue_kt = 0;
-    auto issue_next = [&](int slot) {
-        FA3_LDS char* nb = smem + slot * C::kQBuf;
-        load_tile_async<D>(nb, kh + (size_t)issue_kt * 64 * D, ld_off, w);
-        load_tile_async<D>(nb + C::kTileBytes, vh + (size_t)issue_kt * 64 * D, ld_off, w);
-        ++issue_kt;
+    int ld_kt = 0;
+    auto issue = [&](FA3_LDS char* st) {
+        load_tile_async<D>(st, kh + (size_t)ld_kt * 64 * D, ld_off, w);
+        load_tile_async<D>(st + C::kTileBytes, vh + (size_t)ld_kt * 64 * D, ld_off, w);
+        if (ld_kt + 1 < n_kt) ++ld_kt;
     };
-    auto wait_tiles = [&](int tiles) {
-        if (tiles >= 2) wait_vmcnt<2 * (2 * C::kLoadsPerWave)>();
-        else if (tiles == 1) wait_vmcnt<2 * C::kLoadsPerWave>();
-        else wait_vmcnt<0>();
-    };
-    // S^T, dP^T: lane holds q = 32wq + l32, key = 32wk + 8(i/4) + 4h + i%4
-    auto stage_a = [&](FA3_LDS char* buf, f32x16& sacc, f32x16& pacc) {
-        sacc = f32x16{};
-        pacc = f32x16{};
+
+    // B operands: row 32 rh + 16 rb + l16, D chunk p1_chunk(s, g4)
+    f16x8 qf[2][C::kKs], df[2][C::kKs];
+    float l2[2];
+    f32x4 ndl[2];  // -delta of the lane's two rows, the dP^T accumulators' start
+    f32x16 acc[2];
+    acc[0] = f32x16{};
+    acc[1] = f32x16{};
+    // S^T and dP^T - delta of keys 16 kq + 4 g4 + i, rows 32 rh + 16 rb + l16
+    f32x4 sacc[2], pacc[2];
+
+    auto p1_read = [&](const FA3_LDS char* st, f16x8 (&ak)[C::kKs], f16x8 (&av)[C::kKs]) {
 #pragma unroll
-        for (int s = 0; s < C::kKSteps; ++s) {
-            const uint32_t off = tile_off<D>(32 * wk + l32, 2 * s + h);
-            sacc = mfma_32x32x16(lds_read_b128(buf, off), qf[s], sacc);
-            pacc = mfma_32x32x16(lds_read_b128(buf + C::kTileBytes, off), df[s], pacc);
+        for (int s = 0; s < C::kKs; ++s) {
+            const uint32_t off = tile_off<D>(16 * kq + l16, p1_chunk<D>(s, g4));
+            ak[s] = lds_read_b128(st, off);
+            av[s] = lds_read_b128(st + C::kTileBytes, off);
         }
     };
-    auto stage_b = [&](auto masked, const f32x16& sacc, const f32x16& pacc, f16x8 (&dsb)[2]) {
+    // S^T = K Q^T, dP^T - delta = V dO^T - delta
+    auto p1_mfma = [&](const f16x8 (&ak)[C::kKs], const f16x8 (&av)[C::kKs]) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float p = fast_exp2(sacc[i] * a.scale_log2 - l2);
-            if constexpr (decltype(masked)::value) {
-                if (32 * wk + 8 * (i >> 2) + 4 * h + (i & 3) > 32 * wq + l32) p = 0.f;
-            }
-            dsb[i >> 3][i & 7] = (_Float16)(p * (pacc[i] - delta_row));
-        }
-    };
-    // dQ^T += K^T dS^T; A = K^T by transposed reads, key order matching dsb
-    auto stage_c = [&](FA3_LDS char* buf, const f16x8 (&dsb)[2]) {
+        for (int s = 0; s < C::kKs; ++s) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-            for (int mb = 0; mb < C::kMB; ++mb) {
-                f16x4 ak[2];
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const int krow = 32 * wk + 16 * ks + 8 * u + 4 * h + (r16 >> 2);
-                    const int col = 32 * mb + 16 * (g & 1) + 4 * (r16 & 3);
-                    ak[u] = lds_read_tr4(buf, tile_off<D>(krow, col >> 3) + (col & 7) * 2);
-                }
-                dqt[mb] = mfma_32x32x16(concat4(ak[0], ak[1]), dsb[ks], dqt[mb]);
+            for (int rb = 0; rb < 2; ++rb) {
+                sacc[rb] = mfma_16x16x32(ak[s], qf[rb][s], s == 0 ? f32x4{} : sacc[rb]);
+                pacc[rb] = mfma_16x16x32(av[s], df[rb][s], s == 0 ? ndl[rb] : pacc[rb]);
             }
         }
     };
-
-    auto step = [&](auto masked, int kt, f32x16& sacc, f32x16& pacc) {
-        const int slot = kt & (kNBuf - 1);
-        if (kt + 1 < n_kt) {
-            wait_tiles(kt + 2 < n_kt ? 1 : 0);
-            __builtin_amdgcn_s_barrier();
-            if (kt + 3 < n_kt) issue_next((kt + 3) & (kNBuf - 1));
+    // phase-2 A operands (K^T) of the key tile in `st`
+    auto read_xt = [&](const FA3_LDS char* st, f16x8 (&xt)[C::kStepsQ]) {
+#pragma unroll
+        for (int j = 0; j < C::kStepsQ; ++j) xt[j] = tile_read_t<D>(st, db, ks0 + j, lane);
+    };
+    // phase-2 B operands: dS^T rows 32 rb + l32
+    auto read_ds = [&](const FA3_LDS char* ds, f16x8 (&bd)[C::kStepsQ][2]) {
+#pragma unroll
+        for (int j = 0; j < C::kStepsQ; ++j)
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+                bd[j][rb] = lds_read_b128(ds, dst_off(32 * rb + l32, 2 * (ks0 + j) + h));
+    };
+    // softmax element e = 4 rb + i: dS = exp2(S c - lse2) (dP - delta)
+    auto sm_elem = [&](int e, float (&p)[8]) {
+        const int rb = e >> 2, i = e & 3;
+        p[e] = fast_exp2(sacc[rb][i] * a.scale_log2 - l2[rb]) * pacc[rb][i];
+    };
+    // causal mask (diagonal tile only), fp16 dS written row-major ([row][key])
+    auto store_ds = [&](bool masked, float (&p)[8], FA3_LDS char* ds) {
+        if (masked) {
+            __asm__ volatile("" ::: "memory");  // keep this a branch
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (16 * kq + 4 * g4 + (e & 3) > 32 * rh + 16 * (e >> 2) + l16) p[e] = 0.f;
         }
-        __builtin_amdgcn_sched_barrier(0);
-        f16x8 dsb[2];
-        stage_b(masked, sacc, pacc, dsb);
-        stage_a(smem + ((slot + 1) & (kNBuf - 1)) * C::kQBuf, sacc, pacc);
-        stage_c(smem + slot * C::kQBuf, dsb);
-        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            f16x4 dv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dv[i] = (_Float16)p[4 * rb + i];
+            lds_write_b64(ds, pds_off4(32 * rh + 16 * rb + l16, 4 * kq + g4), dv);
+        }
     };
 
-    const int pre = n_kt < 3 ? n_kt : 3;
-    for (int i = 0; i < pre; ++i) issue_next(i);
-    wait_tiles(pre - 1);
-    __builtin_amdgcn_s_barrier();
-    f32x16 sacc, pacc;
-    stage_a(smem, sacc, pacc);
-    // key tiles before the last are below the causal diagonal
-    for (int kt = 0; kt + 1 < n_kt; ++kt) step(std::false_type{}, kt, sacc, pacc);
-    if (kCausal) step(std::true_type{}, n_kt - 1, sacc, pacc);
-    else step(std::false_type{}, n_kt - 1, sacc, pacc);
+    // restrict pointers per step: see the dKV role
+    f16x8 xa[C::kStepsQ], xb[C::kStepsQ];
+    auto prologue = [&](FA3_LDS char* __restrict__ s0, FA3_LDS char* __restrict__ s1,
+                        FA3_LDS char* __restrict__ s2, FA3_LDS char* __restrict__ pa) {
+        // this query tile's Q and dO are staged in the dS area, its lse2 and
+        // -delta in the (otherwise unused) rows slot of stage 0
+        load_tile_async<D>(pa, a.q + row0 * D, ld_off, w);
+        load_tile_async<D>(pa + C::kTileBytes, a.dout + row0 * D, ld_off, w);
+        load_rows_async(s0 + 2 * C::kTileBytes, a.lse2, a.ndelta, row0, w, lane);
+        issue(s0);
+        issue(s1);
+        issue(s2);
+        wait_vm_lgkm0<2 * C::kDmaQ>();
+        barrier();
+        const FA3_LDS float* rows = (const FA3_LDS float*)(s0 + 2 * C::kTileBytes);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            const int r = 32 * rh + 16 * rb + l16;
+#pragma unroll
+            for (int s = 0; s < C::kKs; ++s) {
+                const uint32_t off = tile_off<D>(r, p1_chunk<D>(s, g4));
+                qf[rb][s] = lds_read_b128(pa, off);
+                df[rb][s] = lds_read_b128(pa + C::kTileBytes, off);
+            }
+            l2[rb] = rows[r];
+            const float n = rows[64 + r];
+            ndl[rb] = f32x4{n, n, n, n};
+        }
+        f16x8 ak[C::kKs], av[C::kKs];
+        p1_read(s0, ak, av);
+        p1_mfma(ak, av);
+        read_xt(s0, xa);
+        float p[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm_elem(e, p);
+        wait_vm_lgkm0<2 * C::kDmaQ>();  // Q / dO reads done before dS overwrites them
+        barrier();
+        store_ds(kCausal && n_kt == 1, p, pa);
+    };
+    // same block structure as the dKV step
+    auto step = [&](bool masked, FA3_LDS char* __restrict__ ld, const FA3_LDS char* __restrict__ s1,
+                    const FA3_LDS char* __restrict__ prd, FA3_LDS char* __restrict__ pwr,
+                    const f16x8 (&xcur)[C::kStepsQ], f16x8 (&xnext)[C::kStepsQ]) {
+        wait_vm_lgkm0<C::kDmaQ>();
+        barrier();
+        issue(ld);
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 ak[C::kKs], av[C::kKs];
+        p1_read(s1, ak, av);
+        f16x8 bd[C::kStepsQ][2];
+        read_ds(prd, bd);
+        p1_mfma(ak, av);
+        read_xt(s1, xnext);
+        __builtin_amdgcn_sched_barrier(0);
+        float p[8];
+#pragma unroll
+        for (int m = 0; m < kP2; ++m) {
+            acc[m & 1] = mfma_32x32x16(xcur[m >> 1], bd[m >> 1][m & 1], acc[m & 1]);
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) sm_elem(m * kPer + e, p);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        store_ds(masked, p, pwr);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto last = [&](const f16x8 (&xcur)[C::kStepsQ], const FA3_LDS char* __restrict__ prd) {
+        wait_vm_lgkm0<C::kDmaQ>();
+        barrier();
+        f16x8 bd[C::kStepsQ][2];
+        read_ds(prd, bd);
+#pragma unroll
+        for (int m = 0; m < kP2; ++m)
+            acc[m & 1] = mfma_32x32x16(xcur[m >> 1], bd[m >> 1][m & 1], acc[m & 1]);
+    };
 
-    // Combine the two key-half partials; lane: q = 32wq + l32,
-    // d = 32mb + 8(i/4) + 4h + i%4.
-    FA3_LDS float* xch = (FA3_LDS float*)smem + wq * (C::kMB * 16 * 64);
-    __syncthreads();
-    if (wk == 1) {
-#pragma unroll
-        for (int mb = 0; mb < C::kMB; ++mb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) xch[(mb * 16 + i) * 64 + lane] = dqt[mb][i];
+    FA3_LDS char* st_ld = smem;
+    FA3_LDS char* st_1 = smem + C::kStageBytes;
+    FA3_LDS char* st_2 = smem + 2 * C::kStageBytes;
+    auto rotate = [&]() {
+        FA3_LDS char* t = st_ld;
+        st_ld = st_1;
+        st_1 = st_2;
+        st_2 = t;
+    };
+    FA3_LDS char* ds0 = smem + C::kPdsOff;
+    FA3_LDS char* ds1 = ds0 + 2 * C::kPdsBytes;
+
+    // step j computes the softmax of key tile j + 1; the causal diagonal is
+    // the last key tile
+    prologue(st_ld, st_1, st_2, ds0);
+    int j = 0;
+    for (; j + 2 < n_kt; j += 2) {
+        step(kCausal && j + 2 == n_kt, st_ld, st_1, ds0, ds1, xa, xb);
+        rotate();
+        step(kCausal && j + 3 == n_kt, st_ld, st_1, ds1, ds0, xb, xa);
+        rotate();
     }
-    __syncthreads();
-    if (wk == 0) {
-        _Float16* dqp = a.dq + row * D;
+    if (j + 1 < n_kt) {
+        step(kCausal, st_ld, st_1, ds0, ds1, xa, xb);
+        last(xb, ds1);
+    } else {
+        last(xa, ds0);
+    }
+
+    // Epilogue: add the contraction-split partials through LDS in a fixed
+    // order, then store; lane: row 32 rb + l32, d = 32 db + 8 (i / 4) + 4 h + i % 4.
+    wait_vm_lgkm0<0>();
+    barrier();
+    FA3_LDS float* xch = (FA3_LDS float*)smem + w * (2 * 16 * 64);
+    if (part > 0) {
 #pragma unroll
-        for (int mb = 0; mb < C::kMB; ++mb) {
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xch[(rb * 16 + i) * 64 + lane] = acc[rb][i];
+    }
+    wait_vm_lgkm0<0>();
+    barrier();
+    if (part == 0) {
+#pragma unroll
+        for (int p = 1; p < C::kSplitQ; ++p) {
+            const FA3_LDS float* src = (const FA3_LDS float*)smem + (w + p * C::kDB) * (2 * 16 * 64);
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[rb][i] += src[(rb * 16 + i) * 64 + lane];
+        }
+        _Float16* dqp = a.dq + row0 * D + 32 * db + 4 * h;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
             for (int a4 = 0; a4 < 4; ++a4) {
                 f16x4 o;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int i = 4 * a4 + e;
-                    o[e] = (_Float16)((dqt[mb][i] + xch[(mb * 16 + i) * 64 + lane]) * a.scale);
-                }
-                *(f16x4*)(dqp + 32 * mb + 8 * a4 + 4 * h) = o;
+                for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[rb][4 * a4 + e] * a.scale);
+                *(f16x4*)(dqp + (size_t)(32 * rb + l32) * D + 8 * a4) = o;
             }
         }
     }
@@ -473,7 +738,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, FA3_LDS char* smem)
 // when the shape allows, block id -> (xcd, position) is arranged so that each
 // XCD runs whole parts of groups, keeping a head's tiles in one L2.
 template <int D, bool kCausal>
-__global__ __launch_bounds__(256, 1) void bwd_fused_kernel(FusedArgs a) {
+__global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
     const int id = blockIdx.x;
@@ -503,8 +768,8 @@ __global__ __launch_bounds__(256, 1) void bwd_fused_kernel(FusedArgs a) {
 template <int D>
 void launch_d(const FusedArgs& a, bool causal) {
     const dim3 grid(a.n_groups * a.jobs_per_group);
-    if (causal) hipLaunchKernelGGL((bwd_fused_kernel<D, true>), grid, dim3(256), 0, 0, a);
-    else hipLaunchKernelGGL((bwd_fused_kernel<D, false>), grid, dim3(256), 0, 0, a);
+    if (causal) hipLaunchKernelGGL((bwd_fused_kernel<D, true>), grid, dim3(kThreads), 0, 0, a);
+    else hipLaunchKernelGGL((bwd_fused_kernel<D, false>), grid, dim3(kThreads), 0, 0, a);
 }
 
 }  // namespace
@@ -516,11 +781,10 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     const WorkspacePlan plan = plan_workspace(p);
     char* ws = static_cast<char*>(workspace);
     float* lse2 = reinterpret_cast<float*>(ws + plan.lse2_off);
-    BwdTensors pre = t;
-    if (pre.delta == nullptr) pre.delta = reinterpret_cast<float*>(ws + plan.delta_off);
+    float* ndelta = reinterpret_cast<float*>(ws + plan.ndelta_off);
 
     mark(0);
-    hipError_t err = launch_preprocess(p, pre, lse2, nullptr);
+    hipError_t err = launch_preprocess(p, t, lse2, ndelta);
     if (err != hipSuccess) return err;
     mark(1);
 
@@ -530,7 +794,7 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     a.v = (const _Float16*)t.v;
     a.dout = (const _Float16*)t.dout;
     a.lse2 = lse2;
-    a.delta = pre.delta;
+    a.ndelta = ndelta;
     a.dq = (_Float16*)t.dq;
     a.dk = (_Float16*)t.dk;
     a.dv = (_Float16*)t.dv;
@@ -563,8 +827,8 @@ WorkspacePlan plan_workspace(const BwdProblem& p) {
     const size_t rows = (size_t)p.batch * p.heads_q * p.seqlen;
     auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
     w.lse2_off = 0;
-    w.delta_off = align(rows * sizeof(float));
-    w.total = align(w.delta_off + rows * sizeof(float));
+    w.ndelta_off = align(rows * sizeof(float));
+    w.total = align(w.ndelta_off + rows * sizeof(float));
     w.ok = true;
     return w;
 }

@@ -50,10 +50,10 @@ struct BwdTensors {
 constexpr int32_t kStageEventTag = 0x53544745;
 
 // Device workspace the v2 entry asks the caller for: fp32 lse2 rows, then
-// fp32 delta rows (used when the caller passes no softmax_d), 256-B aligned.
+// fp32 -delta rows, 256-B aligned.
 struct WorkspacePlan {
     size_t lse2_off = 0;
-    size_t delta_off = 0;
+    size_t ndelta_off = 0;
     size_t total = 0;
     bool ok = false;
 };
@@ -64,8 +64,10 @@ WorkspacePlan plan_workspace(const BwdProblem& p);
 // main kernel.
 hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace);
 
-// Delta preprocess only (the component entry shaobo_fa3_bwd_dot_do_o).
+// Delta preprocess: delta into t.delta, lse2 and -delta into the given rows;
+// any of the three may be null.  Alone, it is the component entry
+// shaobo_fa3_bwd_dot_do_o.
 hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
-                             float* dq_acc_to_clear);
+                             float* ndelta);
 
 }  // namespace fa3

@@ -5,10 +5,11 @@
 //   delta[r] = sum_d fp32(dO[r, d]) * fp32(O[r, d])          (fp32)
 //   lse2[r]  = LSE[r] * log2(e)                                 (LSE input)
 //            = max[r] * scale * log2(e) + log2(sum[r])          (SMAX_SSUM)
-// so the main kernel forms P = exp2(s * scale * log2(e) - lse2[r]).
+// so the main kernel forms P = exp2(s * scale * log2(e) - lse2[r]); it also
+// takes -delta[r] (ndelta), which seeds its dP accumulators so that they end
+// at dP - delta.  Each output is optional (null pointer: not written).
 // Optionally also writes the reference's packed sidecar
-// [row_max_log2, row_inv_sum, delta] (reference src/dot_do_o_kernel.cpp:49-61)
-// and clears the fp32 dQ accumulator rows that the main kernel adds into.
+// [row_max_log2, row_inv_sum, delta] (reference src/dot_do_o_kernel.cpp:49-61).
 //
 // HBM-bound: one 16-byte load of dO and of O per lane (D / 8 lanes per row),
 // an in-register dot, and a butterfly reduction over the row's lanes.
@@ -22,8 +23,8 @@ template <int D, bool kLse>
 __global__ __launch_bounds__(256) void preprocess_kernel(
     const _Float16* __restrict__ dout, const _Float16* __restrict__ out,
     const float* __restrict__ aux0, const float* __restrict__ aux1,
-    float* __restrict__ delta, float* __restrict__ lse2, float* __restrict__ packed,
-    float* __restrict__ dq_acc, int rows, float scale_log2) {
+    float* __restrict__ delta, float* __restrict__ lse2, float* __restrict__ ndelta,
+    float* __restrict__ packed, int rows, float scale_log2) {
     constexpr int kLanesPerRow = D / 8;
     constexpr int kRowsPerBlock = 256 / kLanesPerRow;
     const int sub = threadIdx.x % kLanesPerRow;
@@ -39,11 +40,6 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
 #pragma unroll
     for (int off = kLanesPerRow / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kLanesPerRow);
 
-    if (dq_acc != nullptr) {
-        f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        *(f32x4*)(dq_acc + base) = z;
-        *(f32x4*)(dq_acc + base + 4) = z;
-    }
     if (sub == 0) {
         float l2, max_log2, inv_sum;
         if constexpr (kLse) {
@@ -56,8 +52,9 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
             inv_sum = s != 0.f ? 1.f / s : 0.f;
             l2 = max_log2 + log2f(s);
         }
-        delta[row] = acc;
+        if (delta != nullptr) delta[row] = acc;
         if (lse2 != nullptr) lse2[row] = l2;
+        if (ndelta != nullptr) ndelta[row] = -acc;
         if (packed != nullptr) {
             packed[(size_t)row * 3 + 0] = max_log2;
             packed[(size_t)row * 3 + 1] = inv_sum;
@@ -67,7 +64,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
 }
 
 template <int D>
-hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, float* dq_acc) {
+hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta) {
     constexpr int kRowsPerBlock = 256 / (D / 8);
     const int rows = p.batch * p.heads_q * p.seqlen;
     const int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
@@ -75,11 +72,11 @@ hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, f
     if (t.aux_is_lse) {
         hipLaunchKernelGGL((preprocess_kernel<D, true>), dim3(blocks), dim3(256), 0, 0,
                            (const _Float16*)t.dout, (const _Float16*)t.out, t.aux0, t.aux1,
-                           t.delta, lse2, t.packed, dq_acc, rows, scale_log2);
+                           t.delta, lse2, ndelta, t.packed, rows, scale_log2);
     } else {
         hipLaunchKernelGGL((preprocess_kernel<D, false>), dim3(blocks), dim3(256), 0, 0,
                            (const _Float16*)t.dout, (const _Float16*)t.out, t.aux0, t.aux1,
-                           t.delta, lse2, t.packed, dq_acc, rows, scale_log2);
+                           t.delta, lse2, ndelta, t.packed, rows, scale_log2);
     }
     return hipGetLastError();
 }
@@ -87,9 +84,9 @@ hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, f
 }  // namespace
 
 hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
-                             float* dq_acc_to_clear) {
-    if (p.head_dim == 128) return launch_pre_d<128>(p, t, lse2, dq_acc_to_clear);
-    if (p.head_dim == 64) return launch_pre_d<64>(p, t, lse2, dq_acc_to_clear);
+                             float* ndelta) {
+    if (p.head_dim == 128) return launch_pre_d<128>(p, t, lse2, ndelta);
+    if (p.head_dim == 64) return launch_pre_d<64>(p, t, lse2, ndelta);
     return hipErrorInvalidValue;
 }
 
