@@ -208,17 +208,8 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t = w & 3;
     const int l16 = lane & 15, g4 = lane >> 4, l32 = lane & 31, h = lane >> 5;
-    // phase 1: query rows 16 rs .. +16, keys 32 kh .. +32 (two 16-key blocks)
-    const int rs = w & 3, kh = w >> 2;
-    // phase 2: matrix (0: dV from dO and P, 1: dK from Q and dS), D slice db,
-    // contraction steps ks0 .. ks0 + kStepsKv of each tile
-    const int pair = w % C::kPairsKv;
-    const int mat = pair / C::kDB, db = pair % C::kDB;
-    const int part = w / C::kPairsKv;
-    const int ks0 = part * C::kStepsKv;
-    constexpr int kP2 = 2 * C::kStepsKv;  // phase-2 MFMAs per step
-    constexpr int kPer = 8 / kP2;         // softmax elements paired with each
 
     const int S = a.seqlen;
     const int QT = S / 64;
@@ -234,7 +225,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem
 
     // Cursor of the next query tile to load; a finished stream keeps
     // re-loading its last tile (into a stage nobody reads), so every step
-    // issues the same loads.
+    // issues the same loads.  All eight waves take part in every load.
     int ld_bhq = b * a.heads_q + hkv * group, ld_qt = qt0, ld_left = n_it;
     auto issue = [&](FA3_LDS char* st) {
         const size_t row0 = (size_t)ld_bhq * S + ld_qt * 64;
@@ -248,240 +239,227 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem
             }
         }
     };
-    // query tile of the next softmax: the causal diagonal needs the mask
-    int sm_qt = qt0;
-    auto next_masked = [&]() {
-        const bool m = kCausal && sm_qt == kt;
-        if (++sm_qt == QT) sm_qt = qt0;
-        return m;
-    };
-
-    // B operands: key 32 kh + 16 kb + l16, D chunk p1_chunk(s, g4)
-    f16x8 kf[2][C::kKs], vf[2][C::kKs];
-    f32x16 acc[2];
-    acc[0] = f32x16{};
-    acc[1] = f32x16{};
-    // S and dP - delta of rows 16 rs + 4 g4 + i, keys 32 kh + 16 kb + l16
-    f32x4 sacc[2], pacc[2];
-
-    // phase-1 A operands (Q, dO rows 16 rs + l16) and lse2 / -delta of the
-    // lane's rows, from the stage of one tile
-    auto p1_read = [&](const FA3_LDS char* st, f16x8 (&aq)[C::kKs], f16x8 (&ad)[C::kKs],
-                       f32x4& l2, f32x4& ndl) {
-#pragma unroll
-        for (int s = 0; s < C::kKs; ++s) {
-            const uint32_t off = tile_off<D>(16 * rs + l16, p1_chunk<D>(s, g4));
-            aq[s] = lds_read_b128(st, off);
-            ad[s] = lds_read_b128(st + C::kTileBytes, off);
-        }
-        const FA3_LDS char* r = st + 2 * C::kTileBytes + (16 * rs + 4 * g4) * 4;
-        l2 = *(const FA3_LDS f32x4*)r;
-        ndl = *(const FA3_LDS f32x4*)(r + 256);
-    };
-    // S = Q K^T and dP - delta = dO V^T - delta (the accumulator starts at -delta)
-    auto p1_mfma = [&](const f16x8 (&aq)[C::kKs], const f16x8 (&ad)[C::kKs], const f32x4& ndl) {
-#pragma unroll
-        for (int s = 0; s < C::kKs; ++s) {
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                sacc[kb] = mfma_16x16x32(aq[s], kf[kb][s], s == 0 ? f32x4{} : sacc[kb]);
-                pacc[kb] = mfma_16x16x32(ad[s], vf[kb][s], s == 0 ? ndl : pacc[kb]);
-            }
-        }
-    };
-    // phase-2 A operands of the tile in `st`: dO^T (dV waves) or Q^T (dK waves)
-    auto read_xt = [&](const FA3_LDS char* st, f16x8 (&xt)[C::kStepsKv]) {
-        const FA3_LDS char* x = st + (mat == 0 ? C::kTileBytes : 0);
-#pragma unroll
-        for (int j = 0; j < C::kStepsKv; ++j) xt[j] = tile_read_t<D>(x, db, ks0 + j, lane);
-    };
-    // phase-2 B operands: P (dV waves) or dS (dK waves), keys 32 kb + l32
-    auto read_pds = [&](const FA3_LDS char* pds, f16x8 (&bp)[C::kStepsKv][2]) {
-        const FA3_LDS char* pm = pds + mat * C::kPdsBytes;
-#pragma unroll
-        for (int j = 0; j < C::kStepsKv; ++j)
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-                bp[j][kb] = lds_read_b128(pm, dst_off(32 * kb + l32, 2 * (ks0 + j) + h));
-    };
-    // softmax element e = 4 kb + i: P = exp2(S c - lse2), dS = P (dP - delta)
-    auto sm_elem = [&](int e, const f32x4& l2, float (&p)[8], float (&ds)[8]) {
-        const int kb = e >> 2, i = e & 3;
-        p[e] = fast_exp2(sacc[kb][i] * a.scale_log2 - l2[i]);
-        ds[e] = p[e] * pacc[kb][i];
-    };
-    // causal mask (diagonal tile only), fp16 P / dS written transposed
-    // ([key][row]) into the P / dS buffer
-    auto store_pds = [&](bool masked, float (&p)[8], float (&ds)[8], FA3_LDS char* pds) {
-        if (masked) {
-            __asm__ volatile("" ::: "memory");  // keep this a branch: off the diagonal it is skipped
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                if (32 * kh + 16 * (e >> 2) + l16 > 16 * rs + 4 * g4 + (e & 3)) {
-                    p[e] = 0.f;
-                    ds[e] = 0.f;
-                }
-            }
-        }
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            f16x4 pv, dv;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pv[i] = (_Float16)p[4 * kb + i];
-                dv[i] = (_Float16)ds[4 * kb + i];
-            }
-            const uint32_t off = pds_off4(32 * kh + 16 * kb + l16, 4 * rs + g4);
-            lds_write_b64(pds, off, pv);
-            lds_write_b64(pds + C::kPdsBytes, off, dv);
-        }
-    };
-
-    // The LDS regions a step touches are passed as restrict pointers, so the
-    // compiler can tell that its reads do not depend on the direct-to-LDS
-    // loads into other regions and adds no wait for those loads.
-    f16x8 xa[C::kStepsKv], xb[C::kStepsKv];
-    auto prologue = [&](FA3_LDS char* __restrict__ s0, FA3_LDS char* __restrict__ s1,
-                        FA3_LDS char* __restrict__ s2, FA3_LDS char* __restrict__ pa) {
-        // this key tile's K and V are staged in the P / dS area
-        const size_t k0 = (size_t)bkv * S + kbase;
-        load_tile_async<D>(pa, a.k + k0 * D, ld_off, w);
-        load_tile_async<D>(pa + C::kTileBytes, a.v + k0 * D, ld_off, w);
-        issue(s0);
-        issue(s1);
-        issue(s2);
-        wait_vm_lgkm0<2 * C::kDmaKv>();
-        barrier();
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int s = 0; s < C::kKs; ++s) {
-                const uint32_t off = tile_off<D>(32 * kh + 16 * kb + l16, p1_chunk<D>(s, g4));
-                kf[kb][s] = lds_read_b128(pa, off);
-                vf[kb][s] = lds_read_b128(pa + C::kTileBytes, off);
-            }
-        f16x8 aq[C::kKs], ad[C::kKs];
-        f32x4 l2, ndl;
-        p1_read(s0, aq, ad, l2, ndl);
-        p1_mfma(aq, ad, ndl);
-        read_xt(s0, xa);
-        float p[8], ds[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sm_elem(e, l2, p, ds);
-        wait_vm_lgkm0<2 * C::kDmaKv>();  // K / V reads done before P / dS overwrite them
-        barrier();
-        store_pds(next_masked(), p, ds, pa);
-    };
-    // Step j: tile j + 1 landed everywhere and P / dS of tile j are written;
-    // the stage of tile j (read during step j - 1) is free for tile j + 3.
-    //   A: phase-1 operands of tile j + 1;
-    //   B: its S / dP MFMAs, beside the reads of P / dS (j) and of the
-    //      transposed operands of tile j + 1 (used in step j + 1);
-    //   C: the phase-2 MFMAs of tile j, each with a slice of the softmax of
-    //      tile j + 1, so the MFMA pipe has work while the VALU runs;
-    //   D: mask, pack and write P / dS (j + 1).
-    auto step = [&](FA3_LDS char* __restrict__ ld, const FA3_LDS char* __restrict__ s1,
-                    const FA3_LDS char* __restrict__ prd, FA3_LDS char* __restrict__ pwr,
-                    const f16x8 (&xcur)[C::kStepsKv], f16x8 (&xnext)[C::kStepsKv]) {
+    auto top = [&]() {
         wait_vm_lgkm0<C::kDmaKv>();
         barrier();
-        issue(ld);
-        __builtin_amdgcn_sched_barrier(0);
-        f16x8 aq[C::kKs], ad[C::kKs];
-        f32x4 l2, ndl;
-        p1_read(s1, aq, ad, l2, ndl);
-        f16x8 bp[C::kStepsKv][2];
-        read_pds(prd, bp);
-        p1_mfma(aq, ad, ndl);
-        read_xt(s1, xnext);
-        __builtin_amdgcn_sched_barrier(0);
-        float p[8], ds[8];
-#pragma unroll
-        for (int m = 0; m < kP2; ++m) {
-            acc[m & 1] = mfma_32x32x16(xcur[m >> 1], bp[m >> 1][m & 1], acc[m & 1]);
-#pragma unroll
-            for (int e = 0; e < kPer; ++e) sm_elem(m * kPer + e, l2, p, ds);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        store_pds(next_masked(), p, ds, pwr);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    auto last = [&](const f16x8 (&xcur)[C::kStepsKv], const FA3_LDS char* __restrict__ prd) {
-        wait_vm_lgkm0<C::kDmaKv>();
-        barrier();
-        f16x8 bp[C::kStepsKv][2];
-        read_pds(prd, bp);
-#pragma unroll
-        for (int m = 0; m < kP2; ++m)
-            acc[m & 1] = mfma_32x32x16(xcur[m >> 1], bp[m >> 1][m & 1], acc[m & 1]);
     };
 
     FA3_LDS char* st_ld = smem;                     // stage of tile j (refilled in step j)
     FA3_LDS char* st_1 = smem + C::kStageBytes;      // stage of tile j + 1
     FA3_LDS char* st_2 = smem + 2 * C::kStageBytes;  // stage of tile j + 2
     auto rotate = [&]() {
-        FA3_LDS char* t = st_ld;
+        FA3_LDS char* x = st_ld;
         st_ld = st_1;
         st_1 = st_2;
-        st_2 = t;
+        st_2 = x;
     };
     FA3_LDS char* pds0 = smem + C::kPdsOff;
     FA3_LDS char* pds1 = pds0 + 2 * C::kPdsBytes;
-
-    prologue(st_ld, st_1, st_2, pds0);
-    int j = 0;
-    for (; j + 2 < n_it; j += 2) {  // two steps per trip: xa / xb alternate
-        step(st_ld, st_1, pds0, pds1, xa, xb);
-        rotate();
-        step(st_ld, st_1, pds1, pds0, xb, xa);
-        rotate();
-    }
-    if (j + 1 < n_it) {
-        step(st_ld, st_1, pds0, pds1, xa, xb);
-        last(xb, pds1);
-    } else {
-        last(xa, pds0);
-    }
-
-    // Epilogue: add the contraction-split partials through LDS in a fixed
-    // order (head dim 64), then store; lane: key 32 kb + l32,
-    // d = 32 db + 8 (i / 4) + 4 h + i % 4.
-    wait_vm_lgkm0<0>();
-    barrier();
-    if constexpr (C::kSplitKv > 1) {
-        FA3_LDS float* xch = (FA3_LDS float*)smem + w * (2 * 16 * 64);
-        if (part > 0) {
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) xch[(kb * 16 + i) * 64 + lane] = acc[kb][i];
-        }
-        wait_vm_lgkm0<0>();
+    auto prologue_loads = [&]() {
+        // this key tile's K and V are staged in the P / dS area
+        const size_t k0 = (size_t)bkv * S + kbase;
+        load_tile_async<D>(pds0, a.k + k0 * D, ld_off, w);
+        load_tile_async<D>(pds0 + C::kTileBytes, a.v + k0 * D, ld_off, w);
+        issue(st_ld);
+        issue(st_1);
+        issue(st_2);
+        wait_vm_lgkm0<2 * C::kDmaKv>();
         barrier();
-        if (part == 0) {
+    };
+
+    if (w < 4) {
+        // ---- score waves: S, dP, P, dS of query rows 16 t .. +16 and all 64
+        // keys (four 16-key blocks); P^T and dS^T go to LDS.
+        // B operands: key 16 kb + l16, D chunk p1_chunk(s, g4)
+        f16x8 kf[4][C::kKs], vf[4][C::kKs];
+        f32x4 sacc[4], pacc[4];  // rows 16 t + 4 g4 + i, keys 16 kb + l16
+        int sm_qt = qt0;         // query tile of the next softmax
+        auto next_masked = [&]() {
+            const bool m = kCausal && sm_qt == kt;
+            if (++sm_qt == QT) sm_qt = qt0;
+            return m;
+        };
+        // S = Q K^T and dP - delta = dO V^T - delta, then P and dS, written
+        // transposed ([key][row]) into the P / dS buffer
+        auto score = [&](bool masked, const FA3_LDS char* st, FA3_LDS char* pds) {
+            f16x8 aq[C::kKs], ad[C::kKs];
 #pragma unroll
-            for (int p = 1; p < C::kSplitKv; ++p) {
-                const FA3_LDS float* src =
-                    (const FA3_LDS float*)smem + (w + p * C::kPairsKv) * (2 * 16 * 64);
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) acc[kb][i] += src[(kb * 16 + i) * 64 + lane];
+            for (int s = 0; s < C::kKs; ++s) {
+                const uint32_t off = tile_off<D>(16 * t + l16, p1_chunk<D>(s, g4));
+                aq[s] = lds_read_b128(st, off);
+                ad[s] = lds_read_b128(st + C::kTileBytes, off);
             }
+            const FA3_LDS char* r = st + 2 * C::kTileBytes + (16 * t + 4 * g4) * 4;
+            const f32x4 l2 = *(const FA3_LDS f32x4*)r;
+            const f32x4 ndl = *(const FA3_LDS f32x4*)(r + 256);
+#pragma unroll
+            for (int s = 0; s < C::kKs; ++s) {
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    sacc[kb] = mfma_16x16x32(aq[s], kf[kb][s], s == 0 ? f32x4{} : sacc[kb]);
+                    pacc[kb] = mfma_16x16x32(ad[s], vf[kb][s], s == 0 ? ndl : pacc[kb]);
+                }
+            }
+            float p[16], ds[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int kb = e >> 2, i = e & 3;
+                p[e] = fast_exp2(sacc[kb][i] * a.scale_log2 - l2[i]);
+                ds[e] = p[e] * pacc[kb][i];
+            }
+            if (masked) {  // causal diagonal tile: keys after the row see nothing
+                __asm__ volatile("" ::: "memory");  // keep this a branch
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    if (16 * (e >> 2) + l16 > 16 * t + 4 * g4 + (e & 3)) {
+                        p[e] = 0.f;
+                        ds[e] = 0.f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                f16x4 pv, dv;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pv[i] = (_Float16)p[4 * kb + i];
+                    dv[i] = (_Float16)ds[4 * kb + i];
+                }
+                const uint32_t off = pds_off4(16 * kb + l16, 4 * t + g4);
+                lds_write_b64(pds, off, pv);
+                lds_write_b64(pds + C::kPdsBytes, off, dv);
+            }
+        };
+        // The LDS regions a step touches are passed as restrict pointers, so
+        // the compiler can tell that its reads do not depend on the
+        // direct-to-LDS loads into other regions and adds no wait for them.
+        auto prologue = [&](FA3_LDS char* __restrict__ s0, FA3_LDS char* __restrict__ pa) {
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int s = 0; s < C::kKs; ++s) {
+                    const uint32_t off = tile_off<D>(16 * kb + l16, p1_chunk<D>(s, g4));
+                    kf[kb][s] = lds_read_b128(pa, off);
+                    vf[kb][s] = lds_read_b128(pa + C::kTileBytes, off);
+                }
+            wait_vm_lgkm0<2 * C::kDmaKv>();  // K / V reads done before P / dS overwrite them
+            barrier();
+            score(next_masked(), s0, pa);
+        };
+        auto step = [&](FA3_LDS char* __restrict__ ld, const FA3_LDS char* __restrict__ s1,
+                        FA3_LDS char* __restrict__ pwr) {
+            top();
+            issue(ld);
+            __builtin_amdgcn_sched_barrier(0);
+            score(next_masked(), s1, pwr);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        prologue_loads();
+        prologue(st_ld, pds0);
+        int j = 0;
+        for (; j + 2 < n_it; j += 2) {
+            step(st_ld, st_1, pds1);
+            rotate();
+            step(st_ld, st_1, pds0);
+            rotate();
         }
-    }
-    if (part == 0) {
-        const float mul = mat == 0 ? 1.f : a.scale;
-        _Float16* outp =
-            (mat == 0 ? a.dv : a.dk) + ((size_t)bkv * S + kbase) * D + 32 * db + 4 * h;
+        if (j + 1 < n_it) step(st_ld, st_1, pds1);
+        top();  // matches the gradient waves' last phase
+    } else {
+        // ---- gradient waves: dV^T and dK^T for D slice(s); wave t owns the
+        // (matrix, slice) pairs u = kPpw t .. +kPpw, matrix = u % 2 (0: dV
+        // from dO and P, 1: dK from Q and dS), slice db = u / 2, over all 64
+        // keys (two 32-key blocks)
+        constexpr int kPpw = C::kDB / 2;
+        f32x16 acc[kPpw][2];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int u = 0; u < kPpw; ++u) {
+            acc[u][0] = f32x16{};
+            acc[u][1] = f32x16{};
+        }
+        // A operands (X^T, X = dO or Q) of a tile: [pair][k-step]
+        f16x8 xa[kPpw][4], xb[kPpw][4];
+        auto read_xt = [&](const FA3_LDS char* st, f16x8 (&xt)[kPpw][4]) {
 #pragma unroll
-            for (int a4 = 0; a4 < 4; ++a4) {
-                f16x4 o;
+            for (int u = 0; u < kPpw; ++u) {
+                const int pu = kPpw * t + u;
+                const FA3_LDS char* x = st + ((pu & 1) == 0 ? C::kTileBytes : 0);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[kb][4 * a4 + e] * mul);
-                *(f16x4*)(outp + (size_t)(32 * kb + l32) * D + 8 * a4) = o;
+                for (int ks = 0; ks < 4; ++ks) xt[u][ks] = tile_read_t<D>(x, pu >> 1, ks, lane);
+            }
+        };
+        // X^T P (or dS) with P / dS read as B operands, keys 32 kb + l32.
+        // All B operands of the step are read before the first MFMA, so one
+        // LDS round trip covers them all.
+        auto grad = [&](const f16x8 (&xt)[kPpw][4], const FA3_LDS char* pds) {
+            f16x8 bp[4][kPpw][2];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int u = 0; u < kPpw; ++u)
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+                        bp[ks][u][kb] = lds_read_b128(pds + ((kPpw * t + u) & 1) * C::kPdsBytes,
+                                                      dst_off(32 * kb + l32, 2 * ks + h));
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int u = 0; u < kPpw; ++u)
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+                        acc[u][kb] = mfma_32x32x16(xt[u][ks], bp[ks][u][kb], acc[u][kb]);
+        };
+        auto prologue = [&](const FA3_LDS char* __restrict__ s0) {
+            read_xt(s0, xa);
+            wait_vm_lgkm0<2 * C::kDmaKv>();
+            barrier();
+        };
+        auto step = [&](FA3_LDS char* __restrict__ ld, const FA3_LDS char* __restrict__ s1,
+                        const FA3_LDS char* __restrict__ prd, const f16x8 (&xcur)[kPpw][4],
+                        f16x8 (&xnext)[kPpw][4]) {
+            top();
+            issue(ld);
+            __builtin_amdgcn_sched_barrier(0);
+            grad(xcur, prd);
+            read_xt(s1, xnext);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        auto last = [&](const f16x8 (&xcur)[kPpw][4], const FA3_LDS char* __restrict__ prd) {
+            top();
+            grad(xcur, prd);
+        };
+        prologue_loads();
+        prologue(st_ld);
+        int j = 0;
+        for (; j + 2 < n_it; j += 2) {
+            step(st_ld, st_1, pds0, xa, xb);
+            rotate();
+            step(st_ld, st_1, pds1, xb, xa);
+            rotate();
+        }
+        if (j + 1 < n_it) {
+            step(st_ld, st_1, pds0, xa, xb);
+            last(xb, pds1);
+        } else {
+            last(xa, pds0);
+        }
+        // store: lane key 32 kb + l32, d = 32 db + 8 (i / 4) + 4 h + i % 4
+#pragma unroll
+        for (int u = 0; u < kPpw; ++u) {
+            const int pu = kPpw * t + u;
+            const float mul = (pu & 1) == 0 ? 1.f : a.scale;
+            _Float16* outp = ((pu & 1) == 0 ? a.dv : a.dk) + ((size_t)bkv * S + kbase) * D +
+                             32 * (pu >> 1) + 4 * h;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4) {
+                    f16x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[u][kb][4 * a4 + e] * mul);
+                    *(f16x4*)(outp + (size_t)(32 * kb + l32) * D + 8 * a4) = o;
+                }
             }
         }
     }
@@ -496,15 +474,8 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, FA3_LDS char* smem)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t = w & 3;
     const int l16 = lane & 15, g4 = lane >> 4, l32 = lane & 31, h = lane >> 5;
-    // phase 1: keys 16 kq .. +16, query rows 32 rh .. +32 (two 16-row blocks)
-    const int kq = w & 3, rh = w >> 2;
-    // phase 2: D slice db, contraction steps ks0 .. ks0 + kStepsQ of each tile
-    const int db = w % C::kDB;
-    const int part = w / C::kDB;
-    const int ks0 = part * C::kStepsQ;
-    constexpr int kP2 = 2 * C::kStepsQ;
-    constexpr int kPer = 8 / kP2;
 
     const int S = a.seqlen;
     const int QT = S / 64;
@@ -524,206 +495,190 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, FA3_LDS char* smem)
         load_tile_async<D>(st + C::kTileBytes, vh + (size_t)ld_kt * 64 * D, ld_off, w);
         if (ld_kt + 1 < n_kt) ++ld_kt;
     };
-
-    // B operands: row 32 rh + 16 rb + l16, D chunk p1_chunk(s, g4)
-    f16x8 qf[2][C::kKs], df[2][C::kKs];
-    float l2[2];
-    f32x4 ndl[2];  // -delta of the lane's two rows, the dP^T accumulators' start
-    f32x16 acc[2];
-    acc[0] = f32x16{};
-    acc[1] = f32x16{};
-    // S^T and dP^T - delta of keys 16 kq + 4 g4 + i, rows 32 rh + 16 rb + l16
-    f32x4 sacc[2], pacc[2];
-
-    auto p1_read = [&](const FA3_LDS char* st, f16x8 (&ak)[C::kKs], f16x8 (&av)[C::kKs]) {
-#pragma unroll
-        for (int s = 0; s < C::kKs; ++s) {
-            const uint32_t off = tile_off<D>(16 * kq + l16, p1_chunk<D>(s, g4));
-            ak[s] = lds_read_b128(st, off);
-            av[s] = lds_read_b128(st + C::kTileBytes, off);
-        }
-    };
-    // S^T = K Q^T, dP^T - delta = V dO^T - delta
-    auto p1_mfma = [&](const f16x8 (&ak)[C::kKs], const f16x8 (&av)[C::kKs]) {
-#pragma unroll
-        for (int s = 0; s < C::kKs; ++s) {
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-                sacc[rb] = mfma_16x16x32(ak[s], qf[rb][s], s == 0 ? f32x4{} : sacc[rb]);
-                pacc[rb] = mfma_16x16x32(av[s], df[rb][s], s == 0 ? ndl[rb] : pacc[rb]);
-            }
-        }
-    };
-    // phase-2 A operands (K^T) of the key tile in `st`
-    auto read_xt = [&](const FA3_LDS char* st, f16x8 (&xt)[C::kStepsQ]) {
-#pragma unroll
-        for (int j = 0; j < C::kStepsQ; ++j) xt[j] = tile_read_t<D>(st, db, ks0 + j, lane);
-    };
-    // phase-2 B operands: dS^T rows 32 rb + l32
-    auto read_ds = [&](const FA3_LDS char* ds, f16x8 (&bd)[C::kStepsQ][2]) {
-#pragma unroll
-        for (int j = 0; j < C::kStepsQ; ++j)
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-                bd[j][rb] = lds_read_b128(ds, dst_off(32 * rb + l32, 2 * (ks0 + j) + h));
-    };
-    // softmax element e = 4 rb + i: dS = exp2(S c - lse2) (dP - delta)
-    auto sm_elem = [&](int e, float (&p)[8]) {
-        const int rb = e >> 2, i = e & 3;
-        p[e] = fast_exp2(sacc[rb][i] * a.scale_log2 - l2[rb]) * pacc[rb][i];
-    };
-    // causal mask (diagonal tile only), fp16 dS written row-major ([row][key])
-    auto store_ds = [&](bool masked, float (&p)[8], FA3_LDS char* ds) {
-        if (masked) {
-            __asm__ volatile("" ::: "memory");  // keep this a branch
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (16 * kq + 4 * g4 + (e & 3) > 32 * rh + 16 * (e >> 2) + l16) p[e] = 0.f;
-        }
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            f16x4 dv;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dv[i] = (_Float16)p[4 * rb + i];
-            lds_write_b64(ds, pds_off4(32 * rh + 16 * rb + l16, 4 * kq + g4), dv);
-        }
-    };
-
-    // restrict pointers per step: see the dKV role
-    f16x8 xa[C::kStepsQ], xb[C::kStepsQ];
-    auto prologue = [&](FA3_LDS char* __restrict__ s0, FA3_LDS char* __restrict__ s1,
-                        FA3_LDS char* __restrict__ s2, FA3_LDS char* __restrict__ pa) {
-        // this query tile's Q and dO are staged in the dS area, its lse2 and
-        // -delta in the (otherwise unused) rows slot of stage 0
-        load_tile_async<D>(pa, a.q + row0 * D, ld_off, w);
-        load_tile_async<D>(pa + C::kTileBytes, a.dout + row0 * D, ld_off, w);
-        load_rows_async(s0 + 2 * C::kTileBytes, a.lse2, a.ndelta, row0, w, lane);
-        issue(s0);
-        issue(s1);
-        issue(s2);
-        wait_vm_lgkm0<2 * C::kDmaQ>();
-        barrier();
-        const FA3_LDS float* rows = (const FA3_LDS float*)(s0 + 2 * C::kTileBytes);
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            const int r = 32 * rh + 16 * rb + l16;
-#pragma unroll
-            for (int s = 0; s < C::kKs; ++s) {
-                const uint32_t off = tile_off<D>(r, p1_chunk<D>(s, g4));
-                qf[rb][s] = lds_read_b128(pa, off);
-                df[rb][s] = lds_read_b128(pa + C::kTileBytes, off);
-            }
-            l2[rb] = rows[r];
-            const float n = rows[64 + r];
-            ndl[rb] = f32x4{n, n, n, n};
-        }
-        f16x8 ak[C::kKs], av[C::kKs];
-        p1_read(s0, ak, av);
-        p1_mfma(ak, av);
-        read_xt(s0, xa);
-        float p[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sm_elem(e, p);
-        wait_vm_lgkm0<2 * C::kDmaQ>();  // Q / dO reads done before dS overwrites them
-        barrier();
-        store_ds(kCausal && n_kt == 1, p, pa);
-    };
-    // same block structure as the dKV step
-    auto step = [&](bool masked, FA3_LDS char* __restrict__ ld, const FA3_LDS char* __restrict__ s1,
-                    const FA3_LDS char* __restrict__ prd, FA3_LDS char* __restrict__ pwr,
-                    const f16x8 (&xcur)[C::kStepsQ], f16x8 (&xnext)[C::kStepsQ]) {
+    auto top = [&]() {
         wait_vm_lgkm0<C::kDmaQ>();
         barrier();
-        issue(ld);
-        __builtin_amdgcn_sched_barrier(0);
-        f16x8 ak[C::kKs], av[C::kKs];
-        p1_read(s1, ak, av);
-        f16x8 bd[C::kStepsQ][2];
-        read_ds(prd, bd);
-        p1_mfma(ak, av);
-        read_xt(s1, xnext);
-        __builtin_amdgcn_sched_barrier(0);
-        float p[8];
-#pragma unroll
-        for (int m = 0; m < kP2; ++m) {
-            acc[m & 1] = mfma_32x32x16(xcur[m >> 1], bd[m >> 1][m & 1], acc[m & 1]);
-#pragma unroll
-            for (int e = 0; e < kPer; ++e) sm_elem(m * kPer + e, p);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        store_ds(masked, p, pwr);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    auto last = [&](const f16x8 (&xcur)[C::kStepsQ], const FA3_LDS char* __restrict__ prd) {
-        wait_vm_lgkm0<C::kDmaQ>();
-        barrier();
-        f16x8 bd[C::kStepsQ][2];
-        read_ds(prd, bd);
-#pragma unroll
-        for (int m = 0; m < kP2; ++m)
-            acc[m & 1] = mfma_32x32x16(xcur[m >> 1], bd[m >> 1][m & 1], acc[m & 1]);
     };
 
     FA3_LDS char* st_ld = smem;
     FA3_LDS char* st_1 = smem + C::kStageBytes;
     FA3_LDS char* st_2 = smem + 2 * C::kStageBytes;
     auto rotate = [&]() {
-        FA3_LDS char* t = st_ld;
+        FA3_LDS char* x = st_ld;
         st_ld = st_1;
         st_1 = st_2;
-        st_2 = t;
+        st_2 = x;
     };
     FA3_LDS char* ds0 = smem + C::kPdsOff;
     FA3_LDS char* ds1 = ds0 + 2 * C::kPdsBytes;
+    auto prologue_loads = [&]() {
+        // this query tile's Q and dO are staged in the dS area, its lse2 and
+        // -delta in the (otherwise unused) rows slot of stage 0
+        load_tile_async<D>(ds0, a.q + row0 * D, ld_off, w);
+        load_tile_async<D>(ds0 + C::kTileBytes, a.dout + row0 * D, ld_off, w);
+        load_rows_async(st_ld + 2 * C::kTileBytes, a.lse2, a.ndelta, row0, w, lane);
+        issue(st_ld);
+        issue(st_1);
+        issue(st_2);
+        wait_vm_lgkm0<2 * C::kDmaQ>();
+        barrier();
+    };
 
-    // step j computes the softmax of key tile j + 1; the causal diagonal is
-    // the last key tile
-    prologue(st_ld, st_1, st_2, ds0);
-    int j = 0;
-    for (; j + 2 < n_kt; j += 2) {
-        step(kCausal && j + 2 == n_kt, st_ld, st_1, ds0, ds1, xa, xb);
-        rotate();
-        step(kCausal && j + 3 == n_kt, st_ld, st_1, ds1, ds0, xb, xa);
-        rotate();
-    }
-    if (j + 1 < n_kt) {
-        step(kCausal, st_ld, st_1, ds0, ds1, xa, xb);
-        last(xb, ds1);
-    } else {
-        last(xa, ds0);
-    }
-
-    // Epilogue: add the contraction-split partials through LDS in a fixed
-    // order, then store; lane: row 32 rb + l32, d = 32 db + 8 (i / 4) + 4 h + i % 4.
-    wait_vm_lgkm0<0>();
-    barrier();
-    FA3_LDS float* xch = (FA3_LDS float*)smem + w * (2 * 16 * 64);
-    if (part > 0) {
+    if (w < 4) {
+        // ---- score waves: S^T, dP^T, dS^T of keys 16 t .. +16 of each key
+        // tile and all 64 query rows (four 16-row blocks); dS goes to LDS.
+        // B operands: row 16 rb + l16, D chunk p1_chunk(s, g4)
+        f16x8 qf[4][C::kKs], df[4][C::kKs];
+        float l2[4];
+        f32x4 ndl[4];            // -delta of row 16 rb + l16, the dP^T accumulators' start
+        f32x4 sacc[4], pacc[4];  // keys 16 t + 4 g4 + i, rows 16 rb + l16
+        auto score = [&](bool masked, const FA3_LDS char* st, FA3_LDS char* ds) {
+            f16x8 ak[C::kKs], av[C::kKs];
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+            for (int s = 0; s < C::kKs; ++s) {
+                const uint32_t off = tile_off<D>(16 * t + l16, p1_chunk<D>(s, g4));
+                ak[s] = lds_read_b128(st, off);
+                av[s] = lds_read_b128(st + C::kTileBytes, off);
+            }
 #pragma unroll
-            for (int i = 0; i < 16; ++i) xch[(rb * 16 + i) * 64 + lane] = acc[rb][i];
-    }
-    wait_vm_lgkm0<0>();
-    barrier();
-    if (part == 0) {
+            for (int s = 0; s < C::kKs; ++s) {
 #pragma unroll
-        for (int p = 1; p < C::kSplitQ; ++p) {
-            const FA3_LDS float* src = (const FA3_LDS float*)smem + (w + p * C::kDB) * (2 * 16 * 64);
+                for (int rb = 0; rb < 4; ++rb) {
+                    sacc[rb] = mfma_16x16x32(ak[s], qf[rb][s], s == 0 ? f32x4{} : sacc[rb]);
+                    pacc[rb] = mfma_16x16x32(av[s], df[rb][s], s == 0 ? ndl[rb] : pacc[rb]);
+                }
+            }
+            float p[16];
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
+            for (int e = 0; e < 16; ++e) {
+                const int rb = e >> 2, i = e & 3;
+                p[e] = fast_exp2(sacc[rb][i] * a.scale_log2 - l2[rb]) * pacc[rb][i];
+            }
+            if (masked) {  // causal diagonal tile
+                __asm__ volatile("" ::: "memory");  // keep this a branch
 #pragma unroll
-                for (int i = 0; i < 16; ++i) acc[rb][i] += src[(rb * 16 + i) * 64 + lane];
+                for (int e = 0; e < 16; ++e)
+                    if (16 * t + 4 * g4 + (e & 3) > 16 * (e >> 2) + l16) p[e] = 0.f;
+            }
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                f16x4 dv;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dv[i] = (_Float16)p[4 * rb + i];
+                lds_write_b64(ds, pds_off4(16 * rb + l16, 4 * t + g4), dv);
+            }
+        };
+        auto prologue = [&](FA3_LDS char* __restrict__ s0, FA3_LDS char* __restrict__ pa) {
+            const FA3_LDS float* rows = (const FA3_LDS float*)(s0 + 2 * C::kTileBytes);
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int r = 16 * rb + l16;
+#pragma unroll
+                for (int s = 0; s < C::kKs; ++s) {
+                    const uint32_t off = tile_off<D>(r, p1_chunk<D>(s, g4));
+                    qf[rb][s] = lds_read_b128(pa, off);
+                    df[rb][s] = lds_read_b128(pa + C::kTileBytes, off);
+                }
+                l2[rb] = rows[r];
+                const float n = rows[64 + r];
+                ndl[rb] = f32x4{n, n, n, n};
+            }
+            wait_vm_lgkm0<2 * C::kDmaQ>();  // Q / dO reads done before dS overwrites them
+            barrier();
+            score(kCausal && n_kt == 1, s0, pa);
+        };
+        // step j computes the dS of key tile j + 1; the causal diagonal is
+        // the last key tile
+        auto step = [&](bool masked, FA3_LDS char* __restrict__ ld,
+                        const FA3_LDS char* __restrict__ s1, FA3_LDS char* __restrict__ pwr) {
+            top();
+            issue(ld);
+            __builtin_amdgcn_sched_barrier(0);
+            score(masked, s1, pwr);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        prologue_loads();
+        prologue(st_ld, ds0);
+        int j = 0;
+        for (; j + 2 < n_kt; j += 2) {
+            step(kCausal && j + 2 == n_kt, st_ld, st_1, ds1);
+            rotate();
+            step(kCausal && j + 3 == n_kt, st_ld, st_1, ds0);
+            rotate();
         }
+        if (j + 1 < n_kt) step(kCausal, st_ld, st_1, ds1);
+        top();  // matches the gradient waves' last phase
+    } else {
+        // ---- gradient waves: dQ^T slice(s) over query rows; D = 128: slice
+        // t, both 32-row blocks; D = 64: slice t / 2, row block t % 2
+        constexpr int kRb = C::kDB / 2;  // 32-row blocks per wave
+        const int db = C::kDB == 4 ? t : t >> 1;
+        const int rb0 = C::kDB == 4 ? 0 : t & 1;
+        f32x16 acc[kRb];
+#pragma unroll
+        for (int r = 0; r < kRb; ++r) acc[r] = f32x16{};
+        f16x8 xa[4], xb[4];  // K^T of a key tile, per k-step
+        auto read_xt = [&](const FA3_LDS char* st, f16x8 (&xt)[4]) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) xt[ks] = tile_read_t<D>(st, db, ks, lane);
+        };
+        auto grad = [&](const f16x8 (&xt)[4], const FA3_LDS char* ds) {
+            f16x8 bd[4][kRb];  // all B operands first: one LDS round trip
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int r = 0; r < kRb; ++r)
+                    bd[ks][r] = lds_read_b128(ds, dst_off(32 * (rb0 + r) + l32, 2 * ks + h));
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int r = 0; r < kRb; ++r) acc[r] = mfma_32x32x16(xt[ks], bd[ks][r], acc[r]);
+        };
+        auto prologue = [&](const FA3_LDS char* __restrict__ s0) {
+            read_xt(s0, xa);
+            wait_vm_lgkm0<2 * C::kDmaQ>();
+            barrier();
+        };
+        auto step = [&](FA3_LDS char* __restrict__ ld, const FA3_LDS char* __restrict__ s1,
+                        const FA3_LDS char* __restrict__ prd, const f16x8 (&xcur)[4],
+                        f16x8 (&xnext)[4]) {
+            top();
+            issue(ld);
+            __builtin_amdgcn_sched_barrier(0);
+            grad(xcur, prd);
+            read_xt(s1, xnext);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        auto last = [&](const f16x8 (&xcur)[4], const FA3_LDS char* __restrict__ prd) {
+            top();
+            grad(xcur, prd);
+        };
+        prologue_loads();
+        prologue(st_ld);
+        int j = 0;
+        for (; j + 2 < n_kt; j += 2) {
+            step(st_ld, st_1, ds0, xa, xb);
+            rotate();
+            step(st_ld, st_1, ds1, xb, xa);
+            rotate();
+        }
+        if (j + 1 < n_kt) {
+            step(st_ld, st_1, ds0, xa, xb);
+            last(xb, ds1);
+        } else {
+            last(xa, ds0);
+        }
+        // store: lane row 32 rb + l32, d = 32 db + 8 (i / 4) + 4 h + i % 4
         _Float16* dqp = a.dq + row0 * D + 32 * db + 4 * h;
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
+        for (int r = 0; r < kRb; ++r) {
 #pragma unroll
             for (int a4 = 0; a4 < 4; ++a4) {
                 f16x4 o;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[rb][4 * a4 + e] * a.scale);
-                *(f16x4*)(dqp + (size_t)(32 * rb + l32) * D + 8 * a4) = o;
+                for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[r][4 * a4 + e] * a.scale);
+                *(f16x4*)(dqp + (size_t)(32 * (rb0 + r) + l32) * D + 8 * a4) = o;
             }
         }
     }
