@@ -66,6 +66,14 @@ struct FusedArgs {
     int part_len;
     float scale_log2;
     float scale;
+    // split plan (bal_m > 0, causal and one query head per KV head): see
+    // bwd_fused_kernel.  Counters and partial sums live in the workspace.
+    int bal_m;
+    int cnt_kv;        // offset of the split dKV jobs' counters in `counters`
+    int cnt_q;         // offset of the split dQ jobs' counters
+    int* counters;
+    float* part_kv;    // [job][piece][wave][register][lane] fp32
+    float* part_q;
 };
 
 constexpr int kWaves = 8;
@@ -200,10 +208,99 @@ __device__ __forceinline__ uint32_t pds_off4(int r, int q) {
 }
 
 // ----------------------------------------------------------------------------
+// Outputs
+// ----------------------------------------------------------------------------
+// dV^T / dK^T accumulators of gradient wave t (pairs kPpw t .. +kPpw, pair =
+// 2 db + matrix) to fp16 dV / dK; lane: key 32 kb + l32,
+// d = 32 db + 8 (i / 4) + 4 h + i % 4.
+template <int D>
+__device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase, int t, int lane,
+                                          const f32x16 (&acc)[D / 64][2]) {
+    constexpr int kPpw = D / 64;
+    const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int u = 0; u < kPpw; ++u) {
+        const int pu = kPpw * t + u;
+        const float mul = (pu & 1) == 0 ? 1.f : a.scale;
+        _Float16* outp = ((pu & 1) == 0 ? a.dv : a.dk) + ((size_t)bkv * a.seqlen + kbase) * D +
+                         32 * (pu >> 1) + 4 * h;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int a4 = 0; a4 < 4; ++a4) {
+                f16x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[u][kb][4 * a4 + e] * mul);
+                *(f16x4*)(outp + (size_t)(32 * kb + l32) * D + 8 * a4) = o;
+            }
+        }
+    }
+}
+
+// dQ^T accumulators of gradient wave t to fp16 dQ; lane: row 32 rb + l32,
+// d = 32 db + 8 (i / 4) + 4 h + i % 4.
+template <int D>
+__device__ __forceinline__ void store_dq(const FusedArgs& a, size_t row0, int t, int lane,
+                                         const f32x16 (&acc)[D / 64]) {
+    constexpr int kRb = D / 64;
+    const int db = D == 128 ? t : t >> 1;
+    const int rb0 = D == 128 ? 0 : t & 1;
+    const int l32 = lane & 31, h = lane >> 5;
+    _Float16* dqp = a.dq + row0 * D + 32 * db + 4 * h;
+#pragma unroll
+    for (int r = 0; r < kRb; ++r) {
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+            f16x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[r][4 * a4 + e] * a.scale);
+            *(f16x4*)(dqp + (size_t)(32 * (rb0 + r) + l32) * D + 8 * a4) = o;
+        }
+    }
+}
+
+// Partial sums of split jobs travel between workgroups (possibly on
+// different XCDs, whose L2 caches are not coherent with each other) through
+// agent-scope atomic stores and loads: those are coherent device-wide by
+// themselves, so no cache-wide writeback / invalidate (which would also
+// evict the tiles every CU of the XCD is streaming) is needed.
+__device__ __forceinline__ void put_partial(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float get_partial(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// End of one piece of a split job, after its partial sums are stored: wait
+// until every wave's partial stores have completed, count the arrival, and
+// return true in every wave of the workgroup that arrives second; that one
+// reads both pieces (after its counter update, so it sees the other piece's
+// completed stores) and adds them in a fixed order, so the result does not
+// depend on which piece arrives last.  The counter was cleared by the
+// preprocess; the last arriver clears it again.
+__device__ __forceinline__ bool finish_split(int* counter, FA3_LDS char* smem) {
+    wait_vm_lgkm0<0>();
+    barrier();
+    FA3_LDS int* flag = (FA3_LDS int*)smem;
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old;
+    }
+    wait_vm_lgkm0<0>();
+    barrier();
+    return *flag == 1;
+}
+
+// ----------------------------------------------------------------------------
 // dKV role
 // ----------------------------------------------------------------------------
+// Streams query tiles [qa, qb) of every query head of the group.  slot < 0:
+// the job is whole and writes dK / dV; otherwise the unit is piece slot & 1
+// of split job slot >> 1 and the pieces' partial sums meet in finish_split.
 template <int D, bool kCausal>
-__device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem) {
+__device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, int slot,
+                         FA3_LDS char* smem) {
     using C = Cfg<D>;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -217,8 +314,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem
     const int b = bkv / a.heads_kv;
     const int hkv = bkv % a.heads_kv;
     const int kbase = kt * 64;
-    const int qt0 = kCausal ? kt : 0;
-    const int n_it = group * (QT - qt0);
+    const int n_it = group * (qb - qa);
 
     uint32_t ld_off[C::kLoadsPerTile];
     tile_load_offsets<D>(ld_off, w, lane);
@@ -226,15 +322,15 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem
     // Cursor of the next query tile to load; a finished stream keeps
     // re-loading its last tile (into a stage nobody reads), so every step
     // issues the same loads.  All eight waves take part in every load.
-    int ld_bhq = b * a.heads_q + hkv * group, ld_qt = qt0, ld_left = n_it;
+    int ld_bhq = b * a.heads_q + hkv * group, ld_qt = qa, ld_left = n_it;
     auto issue = [&](FA3_LDS char* st) {
         const size_t row0 = (size_t)ld_bhq * S + ld_qt * 64;
         load_tile_async<D>(st, a.q + row0 * D, ld_off, w);
         load_tile_async<D>(st + C::kTileBytes, a.dout + row0 * D, ld_off, w);
         load_rows_async(st + 2 * C::kTileBytes, a.lse2, a.ndelta, row0, w, lane);
         if (--ld_left > 0) {
-            if (++ld_qt == QT) {
-                ld_qt = qt0;
+            if (++ld_qt == qb) {
+                ld_qt = qa;
                 ++ld_bhq;
             }
         }
@@ -273,10 +369,10 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem
         // B operands: key 16 kb + l16, D chunk p1_chunk(s, g4)
         f16x8 kf[4][C::kKs], vf[4][C::kKs];
         f32x4 sacc[4], pacc[4];  // rows 16 t + 4 g4 + i, keys 16 kb + l16
-        int sm_qt = qt0;         // query tile of the next softmax
+        int sm_qt = qa;          // query tile of the next softmax
         auto next_masked = [&]() {
             const bool m = kCausal && sm_qt == kt;
-            if (++sm_qt == QT) sm_qt = qt0;
+            if (++sm_qt == qb) sm_qt = qa;
             return m;
         };
         // S = Q K^T and dP - delta = dO V^T - delta, then P and dS, written
@@ -444,23 +540,37 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem
         } else {
             last(xa, pds0);
         }
-        // store: lane key 32 kb + l32, d = 32 db + 8 (i / 4) + 4 h + i % 4
+        if (slot < 0) {
+            store_dkv<D>(a, bkv, kbase, t, lane, acc);
+        } else {
+            // partial sums in register order: [wave][register][lane]
+            float* pp = a.part_kv + ((size_t)slot * 4 + t) * (kPpw * 2 * 16 * 64) + lane;
 #pragma unroll
-        for (int u = 0; u < kPpw; ++u) {
-            const int pu = kPpw * t + u;
-            const float mul = (pu & 1) == 0 ? 1.f : a.scale;
-            _Float16* outp = ((pu & 1) == 0 ? a.dv : a.dk) + ((size_t)bkv * S + kbase) * D +
-                             32 * (pu >> 1) + 4 * h;
+            for (int u = 0; u < kPpw; ++u)
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+                for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int a4 = 0; a4 < 4; ++a4) {
-                    f16x4 o;
+                    for (int i = 0; i < 16; ++i) put_partial(&pp[((u * 2 + kb) * 16 + i) * 64], acc[u][kb][i]);
+        }
+    }
+    if (slot >= 0 && finish_split(a.counters + a.cnt_kv + (slot >> 1), smem)) {
+        if (w >= 4) {
+            // last piece of the job: dK / dV = piece 0 + piece 1
+            constexpr int kPpw = C::kDB / 2;
+            constexpr int kRegs = kPpw * 2 * 16;
+            const float* p0 = a.part_kv + ((size_t)(slot & ~1) * 4 + t) * (kRegs * 64) + lane;
+            const float* p1 = p0 + (size_t)4 * kRegs * 64;
+            f32x16 acc[kPpw][2];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[u][kb][4 * a4 + e] * mul);
-                    *(f16x4*)(outp + (size_t)(32 * kb + l32) * D + 8 * a4) = o;
-                }
-            }
+            for (int u = 0; u < kPpw; ++u)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int r = ((u * 2 + kb) * 16 + i) * 64;
+                        acc[u][kb][i] = get_partial(p0 + r) + get_partial(p1 + r);
+                    }
+            store_dkv<D>(a, bkv, kbase, t, lane, acc);
         }
     }
 }
@@ -468,8 +578,11 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, FA3_LDS char* smem
 // ----------------------------------------------------------------------------
 // dQ role
 // ----------------------------------------------------------------------------
+// Streams key tiles [ka, kb) (the causal diagonal, key tile qt, is masked).
+// slot: as for dkv_role.
 template <int D, bool kCausal>
-__device__ void dq_role(const FusedArgs& a, int bhq, int qt, FA3_LDS char* smem) {
+__device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int slot,
+                        FA3_LDS char* smem) {
     using C = Cfg<D>;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -483,17 +596,17 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, FA3_LDS char* smem)
     const int b = bhq / a.heads_q;
     const int bkv = b * a.heads_kv + (bhq % a.heads_q) / group;
     const size_t row0 = (size_t)bhq * S + qt * 64;
-    const int n_kt = kCausal ? qt + 1 : QT;
+    const int n_kt = kb - ka;
 
     uint32_t ld_off[C::kLoadsPerTile];
     tile_load_offsets<D>(ld_off, w, lane);
     const _Float16* kh = a.k + (size_t)bkv * S * D;
     const _Float16* vh = a.v + (size_t)bkv * S * D;
-    int ld_kt = 0;
+    int ld_kt = ka;
     auto issue = [&](FA3_LDS char* st) {
         load_tile_async<D>(st, kh + (size_t)ld_kt * 64 * D, ld_off, w);
         load_tile_async<D>(st + C::kTileBytes, vh + (size_t)ld_kt * 64 * D, ld_off, w);
-        if (ld_kt + 1 < n_kt) ++ld_kt;
+        if (ld_kt + 1 < kb) ++ld_kt;
     };
     auto top = [&]() {
         wait_vm_lgkm0<C::kDmaQ>();
@@ -585,10 +698,9 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, FA3_LDS char* smem)
             }
             wait_vm_lgkm0<2 * C::kDmaQ>();  // Q / dO reads done before dS overwrites them
             barrier();
-            score(kCausal && n_kt == 1, s0, pa);
+            score(kCausal && ka == qt, s0, pa);
         };
-        // step j computes the dS of key tile j + 1; the causal diagonal is
-        // the last key tile
+        // step j computes the dS of key tile ka + j + 1
         auto step = [&](bool masked, FA3_LDS char* __restrict__ ld,
                         const FA3_LDS char* __restrict__ s1, FA3_LDS char* __restrict__ pwr) {
             top();
@@ -601,12 +713,12 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, FA3_LDS char* smem)
         prologue(st_ld, ds0);
         int j = 0;
         for (; j + 2 < n_kt; j += 2) {
-            step(kCausal && j + 2 == n_kt, st_ld, st_1, ds1);
+            step(kCausal && ka + j + 1 == qt, st_ld, st_1, ds1);
             rotate();
-            step(kCausal && j + 3 == n_kt, st_ld, st_1, ds0);
+            step(kCausal && ka + j + 2 == qt, st_ld, st_1, ds0);
             rotate();
         }
-        if (j + 1 < n_kt) step(kCausal, st_ld, st_1, ds1);
+        if (j + 1 < n_kt) step(kCausal && ka + j + 1 == qt, st_ld, st_1, ds1);
         top();  // matches the gradient waves' last phase
     } else {
         // ---- gradient waves: dQ^T slice(s) over query rows; D = 128: slice
@@ -669,29 +781,56 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, FA3_LDS char* smem)
         } else {
             last(xa, ds0);
         }
-        // store: lane row 32 rb + l32, d = 32 db + 8 (i / 4) + 4 h + i % 4
-        _Float16* dqp = a.dq + row0 * D + 32 * db + 4 * h;
+        if (slot < 0) {
+            store_dq<D>(a, row0, t, lane, acc);
+        } else {
+            float* pp = a.part_q + ((size_t)slot * 4 + t) * (kRb * 16 * 64) + lane;
 #pragma unroll
-        for (int r = 0; r < kRb; ++r) {
+            for (int r = 0; r < kRb; ++r)
 #pragma unroll
-            for (int a4 = 0; a4 < 4; ++a4) {
-                f16x4 o;
+                for (int i = 0; i < 16; ++i) put_partial(&pp[(r * 16 + i) * 64], acc[r][i]);
+        }
+    }
+    if (slot >= 0 && finish_split(a.counters + a.cnt_q + (slot >> 1), smem)) {
+        if (w >= 4) {
+            constexpr int kRb = C::kDB / 2;
+            const float* p0 = a.part_q + ((size_t)(slot & ~1) * 4 + t) * (kRb * 16 * 64) + lane;
+            const float* p1 = p0 + (size_t)4 * kRb * 16 * 64;
+            f32x16 acc[kRb];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[r][4 * a4 + e] * a.scale);
-                *(f16x4*)(dqp + (size_t)(32 * (rb0 + r) + l32) * D + 8 * a4) = o;
-            }
+            for (int r = 0; r < kRb; ++r)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    acc[r][i] = get_partial(p0 + (r * 16 + i) * 64) + get_partial(p1 + (r * 16 + i) * 64);
+            store_dq<D>(a, row0, t, lane, acc);
         }
     }
 }
 
 // Job map.  Jobs are grouped by (batch, kv head) -- a group's dKV jobs and
-// the dQ jobs of its query heads touch only that head's Q, dO, K, V.  Within
-// a group, position p = (level L, slot r) with G + 1 slots per level: slot 0
-// is the dKV job of key tile L, slot r > 0 the dQ job of query head r - 1 at
-// query tile QT - 1 - L, so the dispatch order is longest first (causal).
-// The hardware deals consecutive workgroup ids round-robin to the 8 XCDs;
-// when the shape allows, block id -> (xcd, position) is arranged so that each
-// XCD runs whole parts of groups, keeping a head's tiles in one L2.
+// the dQ jobs of its query heads touch only that head's Q, dO, K, V.  The
+// hardware deals consecutive workgroup ids round-robin to the 8 XCDs; when
+// the shape allows, block id -> (xcd, position) is arranged so that each XCD
+// runs whole parts of groups, keeping a head's tiles in one L2.
+//
+// Default plan: within a group, position p = (level L, slot r) with G + 1
+// slots per level: slot 0 is the dKV job of key tile L, slot r > 0 the dQ
+// job of query head r - 1 at query tile QT - 1 - L, so the dispatch order is
+// longest first (causal).
+//
+// Split plan (bal_m = M = QT / 2 > 0; causal, G = 1, few jobs): the causal
+// jobs run 1 .. QT steps, so one long job would set the kernel's length.
+// Jobs longer than M (dKV key tiles kt < M, dQ query tiles qt >= M) are cut
+// into a head piece of M tiles and a remainder, and each remainder shares a
+// workgroup with a short job of the other role:
+//   p in [0, M):    dKV key tile M + p (whole), then the dQ remainder of
+//                   query tile M + p (key tiles M .. M + p);
+//   p in [M, 2M):   dQ query tile p - M (whole), then the dKV remainder of
+//                   key tile p - M (query tiles p .. QT - 1);
+//   p in [2M, 3M):  dKV head piece of key tile p - 2M (query tiles
+//                   p - 2M .. p - M - 1);
+//   p in [3M, 4M):  dQ head piece of query tile p - 2M (key tiles 0 .. M - 1).
+// Every workgroup runs M or M + 1 steps.
 template <int D, bool kCausal>
 __global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
@@ -710,13 +849,39 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
     }
     const int group = a.heads_q / a.heads_kv;
     const int QT = a.seqlen / 64;
+    if (kCausal && a.bal_m > 0) {
+        // G = 1: group g is query head g (and KV head g)
+        const int M = a.bal_m;
+        const int job0 = g * M;
+        if (pos < M) {
+            dkv_role<D, kCausal>(a, g, M + pos, M + pos, QT, -1, smem);
+            wait_vm_lgkm0<0>();
+            barrier();
+            dq_role<D, kCausal>(a, g, M + pos, M, M + pos + 1, 2 * (job0 + pos) + 1, smem);
+        } else if (pos < 2 * M) {
+            const int x = pos - M;
+            dq_role<D, kCausal>(a, g, x, 0, x + 1, -1, smem);
+            wait_vm_lgkm0<0>();
+            barrier();
+            dkv_role<D, kCausal>(a, g, x, x + M, QT, 2 * (job0 + x) + 1, smem);
+        } else if (pos < 3 * M) {
+            const int x = pos - 2 * M;
+            dkv_role<D, kCausal>(a, g, x, x, x + M, 2 * (job0 + x), smem);
+        } else {
+            const int x = pos - 3 * M;
+            dq_role<D, kCausal>(a, g, M + x, 0, M, 2 * (job0 + x), smem);
+        }
+        return;
+    }
     const int level = pos / (group + 1);
     const int slot = pos % (group + 1);
     if (slot == 0) {
-        dkv_role<D, kCausal>(a, g, level, smem);
+        dkv_role<D, kCausal>(a, g, level, kCausal ? level : 0, QT, -1, smem);
     } else {
         const int b = g / a.heads_kv, hkv = g % a.heads_kv;
-        dq_role<D, kCausal>(a, b * a.heads_q + hkv * group + slot - 1, QT - 1 - level, smem);
+        const int qt = QT - 1 - level;
+        dq_role<D, kCausal>(a, b * a.heads_q + hkv * group + slot - 1, qt, 0, kCausal ? qt + 1 : QT,
+                            -1, smem);
     }
 }
 
@@ -738,8 +903,10 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     float* lse2 = reinterpret_cast<float*>(ws + plan.lse2_off);
     float* ndelta = reinterpret_cast<float*>(ws + plan.ndelta_off);
 
+    int* counters = plan.bal_m > 0 ? reinterpret_cast<int*>(ws + plan.cnt_off) : nullptr;
+
     mark(0);
-    hipError_t err = launch_preprocess(p, t, lse2, ndelta);
+    hipError_t err = launch_preprocess(p, t, lse2, ndelta, counters, plan.n_counters);
     if (err != hipSuccess) return err;
     mark(1);
 
@@ -769,6 +936,12 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     }
     a.scale_log2 = p.scale * kLog2e;
     a.scale = p.scale;
+    a.bal_m = plan.bal_m;
+    a.cnt_kv = 0;
+    a.cnt_q = plan.n_counters / 2;
+    a.counters = counters;
+    a.part_kv = plan.bal_m > 0 ? reinterpret_cast<float*>(ws + plan.pkv_off) : nullptr;
+    a.part_q = plan.bal_m > 0 ? reinterpret_cast<float*>(ws + plan.pq_off) : nullptr;
     if (p.head_dim == 128) launch_d<128>(a, p.causal);
     else launch_d<64>(a, p.causal);
     err = hipGetLastError();
@@ -784,6 +957,21 @@ WorkspacePlan plan_workspace(const BwdProblem& p) {
     w.lse2_off = 0;
     w.ndelta_off = align(rows * sizeof(float));
     w.total = align(w.ndelta_off + rows * sizeof(float));
+    // Split plan for causal shapes with one query head per KV head and few
+    // jobs (at most two per CU of an MI355X): see bwd_fused_kernel.
+    const int qt = p.seqlen / kTileM;
+    const long jobs = 2L * p.batch * p.heads_q * qt;
+    if (p.causal && p.heads_q == p.heads_kv && qt >= 4 && qt % 2 == 0 && jobs <= 512) {
+        w.bal_m = qt / 2;
+        const size_t split_jobs = (size_t)p.batch * p.heads_q * w.bal_m;  // per role
+        const size_t kv_piece = (size_t)4 * (p.head_dim / 64) * 2 * 16 * 64 * sizeof(float);
+        const size_t q_piece = (size_t)4 * (p.head_dim / 64) * 16 * 64 * sizeof(float);
+        w.n_counters = (int)(2 * split_jobs);
+        w.cnt_off = w.total;
+        w.pkv_off = align(w.cnt_off + w.n_counters * sizeof(int));
+        w.pq_off = align(w.pkv_off + split_jobs * 2 * kv_piece);
+        w.total = align(w.pq_off + split_jobs * 2 * q_piece);
+    }
     w.ok = true;
     return w;
 }

@@ -50,10 +50,16 @@ struct BwdTensors {
 constexpr int32_t kStageEventTag = 0x53544745;
 
 // Device workspace the v2 entry asks the caller for: fp32 lse2 rows, then
-// fp32 -delta rows, 256-B aligned.
+// fp32 -delta rows; with the split plan (bal_m > 0) also the split jobs'
+// arrival counters and fp32 partial sums.  Regions are 256-B aligned.
 struct WorkspacePlan {
     size_t lse2_off = 0;
     size_t ndelta_off = 0;
+    int bal_m = 0;          // > 0: split plan with M = bal_m
+    int n_counters = 0;
+    size_t cnt_off = 0;
+    size_t pkv_off = 0;     // dKV pieces' partial sums
+    size_t pq_off = 0;      // dQ pieces' partial sums
     size_t total = 0;
     bool ok = false;
 };
@@ -65,9 +71,9 @@ WorkspacePlan plan_workspace(const BwdProblem& p);
 hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace);
 
 // Delta preprocess: delta into t.delta, lse2 and -delta into the given rows;
-// any of the three may be null.  Alone, it is the component entry
-// shaobo_fa3_bwd_dot_do_o.
+// any of the three may be null; also clears n_counters ints at `counters`.
+// Alone, it is the component entry shaobo_fa3_bwd_dot_do_o.
 hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
-                             float* ndelta);
+                             float* ndelta, int* counters = nullptr, int n_counters = 0);
 
 }  // namespace fa3

@@ -24,9 +24,12 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const _Float16* __restrict__ dout, const _Float16* __restrict__ out,
     const float* __restrict__ aux0, const float* __restrict__ aux1,
     float* __restrict__ delta, float* __restrict__ lse2, float* __restrict__ ndelta,
-    float* __restrict__ packed, int rows, float scale_log2) {
+    float* __restrict__ packed, int* __restrict__ counters, int n_counters, int rows,
+    float scale_log2) {
     constexpr int kLanesPerRow = D / 8;
     constexpr int kRowsPerBlock = 256 / kLanesPerRow;
+    const int gid = blockIdx.x * 256 + threadIdx.x;
+    if (gid < n_counters) counters[gid] = 0;
     const int sub = threadIdx.x % kLanesPerRow;
     const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
     if (row >= rows) return;  // rows % kRowsPerBlock may be non-zero only at the tail
@@ -64,19 +67,23 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
 }
 
 template <int D>
-hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta) {
+hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta,
+                        int* counters, int n_counters) {
     constexpr int kRowsPerBlock = 256 / (D / 8);
     const int rows = p.batch * p.heads_q * p.seqlen;
-    const int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (blocks * 256 < n_counters) blocks = (n_counters + 255) / 256;
     const float scale_log2 = p.scale * kLog2e;
     if (t.aux_is_lse) {
         hipLaunchKernelGGL((preprocess_kernel<D, true>), dim3(blocks), dim3(256), 0, 0,
                            (const _Float16*)t.dout, (const _Float16*)t.out, t.aux0, t.aux1,
-                           t.delta, lse2, ndelta, t.packed, rows, scale_log2);
+                           t.delta, lse2, ndelta, t.packed, counters, n_counters, rows,
+                           scale_log2);
     } else {
         hipLaunchKernelGGL((preprocess_kernel<D, false>), dim3(blocks), dim3(256), 0, 0,
                            (const _Float16*)t.dout, (const _Float16*)t.out, t.aux0, t.aux1,
-                           t.delta, lse2, ndelta, t.packed, rows, scale_log2);
+                           t.delta, lse2, ndelta, t.packed, counters, n_counters, rows,
+                           scale_log2);
     }
     return hipGetLastError();
 }
@@ -84,9 +91,9 @@ hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, f
 }  // namespace
 
 hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
-                             float* ndelta) {
-    if (p.head_dim == 128) return launch_pre_d<128>(p, t, lse2, ndelta);
-    if (p.head_dim == 64) return launch_pre_d<64>(p, t, lse2, ndelta);
+                             float* ndelta, int* counters, int n_counters) {
+    if (p.head_dim == 128) return launch_pre_d<128>(p, t, lse2, ndelta, counters, n_counters);
+    if (p.head_dim == 64) return launch_pre_d<64>(p, t, lse2, ndelta, counters, n_counters);
     return hipErrorInvalidValue;
 }
 

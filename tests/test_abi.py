@@ -164,17 +164,38 @@ def test_status_strings(lib):
     assert lib.shaobo_fa3_status_string(99).decode() == "unknown"
 
 
+def split_plan_bytes(batch, heads, seqlen, head_dim):
+    """Workspace of the split plan (causal, one query head per KV head, at
+    most 512 jobs): lse2 rows, -delta rows, one int counter per split job
+    (B*H*QT/2 per role), then fp32 partial sums of both pieces of every split
+    job -- dK/dV: 4 waves x (D/64 pairs x 2 key blocks x 16) registers x 64
+    lanes, dQ: 4 waves x (D/64 x 16) x 64 -- each region 256-byte aligned."""
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    rows = batch * heads * seqlen
+    m = seqlen // 64 // 2
+    jobs = batch * heads * m
+    off = align(rows * 4) + align(rows * 4)
+    off = align(off + 2 * jobs * 4)
+    off = align(off + jobs * 2 * 4 * (head_dim // 64) * 2 * 16 * 64 * 4)
+    return align(off + jobs * 2 * 4 * (head_dim // 64) * 16 * 64 * 4)
+
+
 def test_workspace_sizes(lib):
-    """fp32 lse2 rows + fp32 delta rows (delta used when softmax_d is NULL),
-    each region 256-byte aligned; the reference contract test requires a
-    non-zero size for a supported shape (fused_bwd_api_contract.cpp:60-63)."""
+    """fp32 lse2 rows + fp32 -delta rows, each region 256-byte aligned, plus
+    the split plan's counters and partial sums where it applies; the
+    reference contract test requires a non-zero size for a supported shape
+    (fused_bwd_api_contract.cpp:60-63)."""
     def ws(**kw):
         p = F.make_params(lib, **kw)
         return lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
-    rows = 1 * 4 * 2048
-    assert ws(batch=1, seqlen=2048, heads_q=4) == 2 * rows * 4
-    assert ws(batch=1, seqlen=2048, heads_q=4, deterministic=True) == 2 * rows * 4
+    # causal MHA with few jobs: split plan
+    assert ws(batch=1, seqlen=2048, heads_q=4) == split_plan_bytes(1, 4, 2048, 128)
+    assert ws(batch=1, seqlen=2048, heads_q=4, deterministic=True) == split_plan_bytes(1, 4, 2048, 128)
+    assert ws(batch=1, seqlen=512, heads_q=2, head_dim=64) == split_plan_bytes(1, 2, 512, 64)
+    # no split: non-causal, GQA, too many jobs, or fewer than four query tiles
     assert ws(batch=2, seqlen=8192, heads_q=16, head_dim=64, causal=False) == 2 * 2 * 16 * 8192 * 4
+    assert ws(batch=2, seqlen=4096, heads_q=32, heads_kv=8) == 2 * 2 * 32 * 4096 * 4
+    assert ws(batch=2, seqlen=4096, heads_q=4) == 2 * 2 * 4 * 4096 * 4
     assert ws(batch=1, seqlen=128, heads_q=1) == 1024
 
 

@@ -70,9 +70,15 @@ def test_v2_gqa_reference_gate_shape():
     check(res, g, reference_gates=True)
 
 
-def test_deterministic_mode_is_bitwise_repeatable():
-    log("[case] deterministic S=1024 Hq4 Hkv2")
-    g = O.golden(1, 4, 2, 1024, 128, True)
+@pytest.mark.parametrize("hq,hkv,s,d", [(4, 2, 1024, 128),   # one launch plan per job
+                                          (2, 2, 1024, 128),   # split plan (causal, G = 1)
+                                          (2, 2, 512, 64)])
+def test_deterministic_mode_is_bitwise_repeatable(hq, hkv, s, d):
+    """No atomics in the sums: two runs agree bit for bit, also when long
+    causal jobs are split in two and their partial sums meet in whichever
+    workgroup finishes second."""
+    log(f"[case] deterministic S={s} Hq{hq} Hkv{hkv} D{d}")
+    g = O.golden(1, hq, hkv, s, d, True)
     r1 = run_v2(g, torch, deterministic=True)
     r2 = run_v2(g, torch, deterministic=True)
     check(r1, g)
