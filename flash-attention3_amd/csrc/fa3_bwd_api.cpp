@@ -165,6 +165,56 @@ size_t workspace_bytes_of(const ShaoboFa3Params* params) {
     return plan.ok ? plan.total : 0;
 }
 
+// ---- component entries ----
+// Reference path ids (include/dkv_contract.h:7-8, include/dq_contract.h:7-8).
+constexpr int kDkvPathCanonical = 5;
+constexpr int kDqPathCanonical = 6;
+
+// Shape / dtype / layout acceptance shared by the dKV and dQ components
+// (reference valid_dkv_shape / valid_dq_shape, src/dkv_kernel.cpp:50-57,
+// src/dq_kernel.cpp:63-70) and their canonical paths (:59-67, :81-89):
+// one query head per KV head, causal, Sq == Sk, whole 128-row tiles.
+bool component_shape_ok(const ShaoboFa3Params* p) {
+    return p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0 && p->num_heads_q > 0 &&
+           head_dim_supported(p->head_dim_qk) && p->head_dim_v == p->head_dim_qk &&
+           p->dtype == SHAOBO_FA3_DTYPE_FP16 && p->layout == SHAOBO_FA3_LAYOUT_BHSD &&
+           p->seqlen_k == p->seqlen_q && p->seqlen_q % kSequenceAlignment == 0 &&
+           p->num_heads_kv == p->num_heads_q && p->causal == 1;
+}
+
+// fused5 acceptance (reference src/fused_bwd_kernel.cpp:1682-1693): fp16 BHSD,
+// Dqk == Dv (64 or 128 here; the reference builds D = 128 only), causal flag,
+// Sq == Sk in whole 128-row tiles, Hq a multiple of Hkv.
+bool fused5_shape_ok(const ShaoboFa3Params* p) {
+    return p->batch > 0 && p->seqlen_q > 0 && p->num_heads_q > 0 &&
+           p->dtype == SHAOBO_FA3_DTYPE_FP16 && p->layout == SHAOBO_FA3_LAYOUT_BHSD &&
+           head_dim_supported(p->head_dim_qk) && p->head_dim_v == p->head_dim_qk &&
+           is_flag(p->causal) && p->seqlen_q == p->seqlen_k &&
+           p->seqlen_q % kSequenceAlignment == 0 && p->num_heads_kv > 0 &&
+           p->num_heads_q % p->num_heads_kv == 0;
+}
+
+// Problem of a component entry: the scale is taken as given (the reference
+// components do not substitute the default).
+fa3::BwdProblem component_problem(const ShaoboFa3Params* p, bool out_f32) {
+    fa3::BwdProblem pr;
+    pr.batch = p->batch;
+    pr.seqlen = p->seqlen_q;
+    pr.heads_q = p->num_heads_q;
+    pr.heads_kv = p->num_heads_kv;
+    pr.head_dim = p->head_dim_qk;
+    pr.causal = p->causal != 0;
+    pr.deterministic = true;
+    pr.scale = p->softmax_scale;
+    pr.out_f32 = out_f32;
+    return pr;
+}
+
+size_t component_workspace(const fa3::BwdProblem& pr) {
+    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr);
+    return plan.ok ? plan.total : 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -274,6 +324,99 @@ int shaobo_fa3_bwd_dot_do_o(const void* dout, const void* out, const void* softm
     t.delta = static_cast<float*>(delta);
     t.packed = static_cast<float*>(packed_sidecar);
     return finish(fa3::launch_preprocess(pr, t, nullptr, nullptr), params);
+}
+
+size_t shaobo_fa3_bwd_fused5_workspace_bytes(const ShaoboFa3Params* params) {
+    if (params == nullptr || !fused5_shape_ok(params)) return 0;
+    return component_workspace(component_problem(params, false));
+}
+
+int shaobo_fa3_bwd_fused5(const void* dout, const void* q, const void* k, const void* v,
+                          const void* packed_sidecar, void* dq, void* dk, void* dv,
+                          const ShaoboFa3Params* params) {
+    if (params == nullptr || dout == nullptr || q == nullptr || k == nullptr || v == nullptr ||
+        packed_sidecar == nullptr || dq == nullptr || dk == nullptr || dv == nullptr) {
+        return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    }
+    if (!fused5_shape_ok(params)) return SHAOBO_FA3_STATUS_UNSUPPORTED;
+    fa3::BwdTensors t;
+    t.dout = dout;
+    t.q = q;
+    t.k = k;
+    t.v = v;
+    t.packed_in = static_cast<const float*>(packed_sidecar);
+    t.dq = dq;
+    t.dk = dk;
+    t.dv = dv;
+    const fa3::BwdProblem pr = component_problem(params, false);
+    const size_t need = component_workspace(pr);
+    if (need == 0 || params->workspace == nullptr || params->workspace_bytes < need) {
+        return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    }
+    return finish(fa3::launch_backward(pr, t, params->workspace), params);
+}
+
+size_t shaobo_fa3_bwd_dkv_workspace_bytes(const ShaoboFa3Params* params) {
+    (void)params;
+    return 0;  // the canonical path reads the sidecar directly
+}
+
+int shaobo_fa3_bwd_dkv(const void* dout, const void* q, const void* k, const void* v,
+                       const void* out, const void* softmax_aux0, const void* softmax_aux1,
+                       void* dq, void* dk, void* dv, const ShaoboFa3Params* params) {
+    (void)out;
+    (void)softmax_aux0;
+    (void)softmax_aux1;
+    (void)dq;
+    if (params == nullptr) return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    if (params->dkv_path != kDkvPathCanonical || !component_shape_ok(params)) {
+        return SHAOBO_FA3_STATUS_UNSUPPORTED;
+    }
+    if (dout == nullptr || q == nullptr || k == nullptr || v == nullptr || dk == nullptr ||
+        dv == nullptr || params->reserved_ptr[3] == nullptr) {
+        return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    }
+    fa3::BwdTensors t;
+    t.dout = dout;
+    t.q = q;
+    t.k = k;
+    t.v = v;
+    t.packed_in = static_cast<const float*>(params->reserved_ptr[3]);
+    t.dk = dk;
+    t.dv = dv;
+    return finish(fa3::launch_component(component_problem(params, true), t, 1), params);
+}
+
+size_t shaobo_fa3_bwd_dq_workspace_bytes(const ShaoboFa3Params* params) {
+    (void)params;
+    return 0;  // the canonical path reads max / sum / delta directly
+}
+
+int shaobo_fa3_bwd_dq(const void* dout, const void* q, const void* k, const void* v,
+                      const void* out, const void* softmax_aux0, const void* softmax_aux1,
+                      void* dq, void* dk, void* dv, const ShaoboFa3Params* params) {
+    (void)out;
+    (void)dk;
+    (void)dv;
+    if (params == nullptr) return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    if (params->dq_path != kDqPathCanonical || !component_shape_ok(params)) {
+        return SHAOBO_FA3_STATUS_UNSUPPORTED;
+    }
+    if (dout == nullptr || q == nullptr || k == nullptr || v == nullptr ||
+        softmax_aux0 == nullptr || softmax_aux1 == nullptr || dq == nullptr ||
+        params->reserved_ptr[0] == nullptr) {
+        return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    }
+    fa3::BwdTensors t;
+    t.dout = dout;
+    t.q = q;
+    t.k = k;
+    t.v = v;
+    t.aux0 = static_cast<const float*>(softmax_aux0);
+    t.aux1 = static_cast<const float*>(softmax_aux1);
+    t.delta_in = static_cast<const float*>(params->reserved_ptr[0]);
+    t.dq = dq;
+    return finish(fa3::launch_component(component_problem(params, true), t, 2), params);
 }
 
 }  // extern "C"

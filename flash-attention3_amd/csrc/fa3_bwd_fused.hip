@@ -48,11 +48,20 @@ struct FusedArgs {
     const _Float16* k;
     const _Float16* v;
     const _Float16* dout;
+    // Row statistics, by row-source mode kRows of the role templates:
+    // 0: lse2 (= LSE log2 e) and -delta arrays written by a preprocess pass;
+    // 1: the packed sidecar [max_log2, inv_sum, delta] per row (dKV only);
+    // 2: raw row max, row sum and delta arrays (dQ only).
     const float* lse2;   // [B*Hq*S]
     const float* ndelta; // [B*Hq*S], -delta
-    _Float16* dq;
-    _Float16* dk;
-    _Float16* dv;
+    const float* packed; // [B*Hq*S][3]
+    const float* smax;   // [B*Hq*S]
+    const float* ssum;
+    const float* delta;
+    void* dq;          // fp16, or fp32 when out_f32
+    void* dk;
+    void* dv;
+    int out_f32;
     int seqlen;
     int heads_q;
     int heads_kv;
@@ -83,7 +92,7 @@ constexpr int kStages = 3;
 template <int D>
 struct Cfg {
     static constexpr int kTileBytes = 64 * D * 2;           // one [64][D] fp16 tile
-    static constexpr int kRowsBytes = 2 * 64 * 4;           // lse2[64], delta[64]
+    static constexpr int kRowsBytes = 1024;  // row statistics of 64 rows (768 B used)
     static constexpr int kStageBytes = 2 * kTileBytes + kRowsBytes;
     static constexpr int kKs = D / 32;                      // 16x16x32 k-steps over D
     static constexpr int kDB = D / 32;                      // 32-wide slices of D
@@ -164,14 +173,34 @@ __device__ __forceinline__ void load_tile_async(FA3_LDS char* tile, const _Float
     }
 }
 
-// Direct-to-LDS copy of the lse2 and -delta values of 64 query rows starting
-// at row0 into rows[0..64) and rows[64..128): wave w moves 16 of them with
-// lanes 0..15 (one dword each), so every wave issues exactly one load.
-__device__ __forceinline__ void load_rows_async(FA3_LDS char* rows, const float* lse2,
-                                                const float* ndelta, size_t row0, int w, int lane) {
-    const float* src = (w < 4 ? lse2 : ndelta) + row0 + 16 * (w & 3) + lane;
-    FA3_LDS char* dst = rows + 256 * (w >> 2) + 64 * (w & 3);
-    if (lane < 16) __builtin_amdgcn_global_load_lds((const void*)src, (FA3_LDS void*)dst, 4, 0, 0);
+// Direct-to-LDS copy of the row statistics of 64 query rows starting at row0;
+// every wave issues exactly one load (one dword per active lane).
+//   kRows 0: lse2 -> rows[0..64), -delta -> rows[64..128); wave w, lanes 0..15.
+//   kRows 1: packed[3 row0 .. 3 row0 + 192) -> rows[0..192) ([row][3]);
+//            wave w, lanes 0..23 move dwords 24 w .. 24 w + 23.
+//   kRows 2: max -> rows[0..64), sum -> rows[64..128), delta -> rows[128..192);
+//            wave w, lanes 0..23 move entries 24 w .. 24 w + 23 of that list.
+template <int kRows>
+__device__ __forceinline__ void load_rows_async(FA3_LDS char* rows, const FusedArgs& a,
+                                                size_t row0, int w, int lane) {
+    if constexpr (kRows == 0) {
+        const float* src = (w < 4 ? a.lse2 : a.ndelta) + row0 + 16 * (w & 3) + lane;
+        FA3_LDS char* dst = rows + 256 * (w >> 2) + 64 * (w & 3);
+        if (lane < 16)
+            __builtin_amdgcn_global_load_lds((const void*)src, (FA3_LDS void*)dst, 4, 0, 0);
+    } else {
+        const int i = 24 * w + lane;
+        const float* src;
+        if constexpr (kRows == 1) {
+            src = a.packed + 3 * row0 + i;
+        } else {
+            const int arr = i >> 6;
+            src = (arr == 0 ? a.smax : arr == 1 ? a.ssum : a.delta) + row0 + (i & 63);
+        }
+        if (lane < 24)
+            __builtin_amdgcn_global_load_lds((const void*)src, (FA3_LDS void*)(rows + 96 * w), 4,
+                                             0, 0);
+    }
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -210,8 +239,21 @@ __device__ __forceinline__ uint32_t pds_off4(int r, int q) {
 // ----------------------------------------------------------------------------
 // Outputs
 // ----------------------------------------------------------------------------
+// Four consecutive output elements (row-major, element offset `off`), fp16
+// or fp32.
+__device__ __forceinline__ void store4(const FusedArgs& a, void* base, size_t off, f32x4 v) {
+    if (a.out_f32) {
+        *(f32x4*)((float*)base + off) = v;
+    } else {
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = (_Float16)v[e];
+        *(f16x4*)((_Float16*)base + off) = o;
+    }
+}
+
 // dV^T / dK^T accumulators of gradient wave t (pairs kPpw t .. +kPpw, pair =
-// 2 db + matrix) to fp16 dV / dK; lane: key 32 kb + l32,
+// 2 db + matrix) to dV / dK; lane: key 32 kb + l32,
 // d = 32 db + 8 (i / 4) + 4 h + i % 4.
 template <int D>
 __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase, int t, int lane,
@@ -222,22 +264,22 @@ __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase
     for (int u = 0; u < kPpw; ++u) {
         const int pu = kPpw * t + u;
         const float mul = (pu & 1) == 0 ? 1.f : a.scale;
-        _Float16* outp = ((pu & 1) == 0 ? a.dv : a.dk) + ((size_t)bkv * a.seqlen + kbase) * D +
-                         32 * (pu >> 1) + 4 * h;
+        void* outp = (pu & 1) == 0 ? a.dv : a.dk;
+        const size_t off0 = ((size_t)bkv * a.seqlen + kbase) * D + 32 * (pu >> 1) + 4 * h;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
             for (int a4 = 0; a4 < 4; ++a4) {
-                f16x4 o;
+                f32x4 v;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[u][kb][4 * a4 + e] * mul);
-                *(f16x4*)(outp + (size_t)(32 * kb + l32) * D + 8 * a4) = o;
+                for (int e = 0; e < 4; ++e) v[e] = acc[u][kb][4 * a4 + e] * mul;
+                store4(a, outp, off0 + (size_t)(32 * kb + l32) * D + 8 * a4, v);
             }
         }
     }
 }
 
-// dQ^T accumulators of gradient wave t to fp16 dQ; lane: row 32 rb + l32,
+// dQ^T accumulators of gradient wave t to dQ; lane: row 32 rb + l32,
 // d = 32 db + 8 (i / 4) + 4 h + i % 4.
 template <int D>
 __device__ __forceinline__ void store_dq(const FusedArgs& a, size_t row0, int t, int lane,
@@ -246,15 +288,15 @@ __device__ __forceinline__ void store_dq(const FusedArgs& a, size_t row0, int t,
     const int db = D == 128 ? t : t >> 1;
     const int rb0 = D == 128 ? 0 : t & 1;
     const int l32 = lane & 31, h = lane >> 5;
-    _Float16* dqp = a.dq + row0 * D + 32 * db + 4 * h;
+    const size_t off0 = row0 * D + 32 * db + 4 * h;
 #pragma unroll
     for (int r = 0; r < kRb; ++r) {
 #pragma unroll
         for (int a4 = 0; a4 < 4; ++a4) {
-            f16x4 o;
+            f32x4 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = (_Float16)(acc[r][4 * a4 + e] * a.scale);
-            *(f16x4*)(dqp + (size_t)(32 * (rb0 + r) + l32) * D + 8 * a4) = o;
+            for (int e = 0; e < 4; ++e) v[e] = acc[r][4 * a4 + e] * a.scale;
+            store4(a, a.dq, off0 + (size_t)(32 * (rb0 + r) + l32) * D + 8 * a4, v);
         }
     }
 }
@@ -298,9 +340,10 @@ __device__ __forceinline__ bool finish_split(int* counter, FA3_LDS char* smem) {
 // Streams query tiles [qa, qb) of every query head of the group.  slot < 0:
 // the job is whole and writes dK / dV; otherwise the unit is piece slot & 1
 // of split job slot >> 1 and the pieces' partial sums meet in finish_split.
-template <int D, bool kCausal>
+template <int D, bool kCausal, int kRows = 0>
 __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, int slot,
                          FA3_LDS char* smem) {
+    static_assert(kRows == 0 || kRows == 1, "dKV rows come as lse2/-delta or packed");
     using C = Cfg<D>;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -327,7 +370,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         const size_t row0 = (size_t)ld_bhq * S + ld_qt * 64;
         load_tile_async<D>(st, a.q + row0 * D, ld_off, w);
         load_tile_async<D>(st + C::kTileBytes, a.dout + row0 * D, ld_off, w);
-        load_rows_async(st + 2 * C::kTileBytes, a.lse2, a.ndelta, row0, w, lane);
+        load_rows_async<kRows>(st + 2 * C::kTileBytes, a, row0, w, lane);
         if (--ld_left > 0) {
             if (++ld_qt == qb) {
                 ld_qt = qa;
@@ -385,9 +428,24 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                 aq[s] = lds_read_b128(st, off);
                 ad[s] = lds_read_b128(st + C::kTileBytes, off);
             }
-            const FA3_LDS char* r = st + 2 * C::kTileBytes + (16 * t + 4 * g4) * 4;
-            const f32x4 l2 = *(const FA3_LDS f32x4*)r;
-            const f32x4 ndl = *(const FA3_LDS f32x4*)(r + 256);
+            f32x4 l2, ndl;  // lse2 and -delta of rows 16 t + 4 g4 + i
+            if constexpr (kRows == 0) {
+                const FA3_LDS char* r = st + 2 * C::kTileBytes + (16 * t + 4 * g4) * 4;
+                l2 = *(const FA3_LDS f32x4*)r;
+                ndl = *(const FA3_LDS f32x4*)(r + 256);
+            } else {
+                // [row][max_log2, inv_sum, delta]: exp2(x - m) * inv = exp2(x - (m - log2 inv))
+                const FA3_LDS f32x4* r =
+                    (const FA3_LDS f32x4*)(st + 2 * C::kTileBytes + (16 * t + 4 * g4) * 12);
+                const f32x4 r0 = r[0], r1 = r[1], r2 = r[2];
+                const float f[12] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1],
+                                     r1[2], r1[3], r2[0], r2[1], r2[2], r2[3]};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    l2[i] = f[3 * i] - __log2f(f[3 * i + 1]);
+                    ndl[i] = -f[3 * i + 2];
+                }
+            }
 #pragma unroll
             for (int s = 0; s < C::kKs; ++s) {
 #pragma unroll
@@ -580,9 +638,10 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
 // ----------------------------------------------------------------------------
 // Streams key tiles [ka, kb) (the causal diagonal, key tile qt, is masked).
 // slot: as for dkv_role.
-template <int D, bool kCausal>
+template <int D, bool kCausal, int kRows = 0>
 __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int slot,
                         FA3_LDS char* smem) {
+    static_assert(kRows == 0 || kRows == 2, "dQ rows come as lse2/-delta or max/sum/delta");
     using C = Cfg<D>;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -629,7 +688,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         // -delta in the (otherwise unused) rows slot of stage 0
         load_tile_async<D>(ds0, a.q + row0 * D, ld_off, w);
         load_tile_async<D>(ds0 + C::kTileBytes, a.dout + row0 * D, ld_off, w);
-        load_rows_async(st_ld + 2 * C::kTileBytes, a.lse2, a.ndelta, row0, w, lane);
+        load_rows_async<kRows>(st_ld + 2 * C::kTileBytes, a, row0, w, lane);
         issue(st_ld);
         issue(st_1);
         issue(st_2);
@@ -692,8 +751,14 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
                     qf[rb][s] = lds_read_b128(pa, off);
                     df[rb][s] = lds_read_b128(pa + C::kTileBytes, off);
                 }
-                l2[rb] = rows[r];
-                const float n = rows[64 + r];
+                float n;
+                if constexpr (kRows == 0) {
+                    l2[rb] = rows[r];
+                    n = rows[64 + r];
+                } else {  // exp2((x - max) c) / sum = exp2(x c - (max c + log2 sum))
+                    l2[rb] = rows[r] * a.scale_log2 + __log2f(rows[64 + r]);
+                    n = -rows[128 + r];
+                }
                 ndl[rb] = f32x4{n, n, n, n};
             }
             wait_vm_lgkm0<2 * C::kDmaQ>();  // Q / dO reads done before dS overwrites them
@@ -831,12 +896,8 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
 //                   p - 2M .. p - M - 1);
 //   p in [3M, 4M):  dQ head piece of query tile p - 2M (key tiles 0 .. M - 1).
 // Every workgroup runs M or M + 1 steps.
-template <int D, bool kCausal>
-__global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
-    __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
-    FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
+__device__ __forceinline__ void job_of(const FusedArgs& a, int& g, int& pos) {
     const int id = blockIdx.x;
-    int g, pos;
     if (a.xcd_parts > 0) {
         const int xcd = id & 7;
         const int n = id >> 3;
@@ -847,6 +908,14 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
         g = id / a.jobs_per_group;
         pos = id % a.jobs_per_group;
     }
+}
+
+template <int D, bool kCausal>
+__global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
+    __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
+    FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
+    int g, pos;
+    job_of(a, g, pos);
     const int group = a.heads_q / a.heads_kv;
     const int QT = a.seqlen / 64;
     if (kCausal && a.bal_m > 0) {
@@ -885,6 +954,25 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
     }
 }
 
+// Single-role grids of the dK/dV and dQ components (causal, one query head
+// per KV head, fp32 outputs): one job per key tile (kRole 1, row statistics
+// from the packed sidecar) or per query tile (kRole 2, from max / sum /
+// delta), longest first.  No workspace: the statistics are folded in LDS.
+template <int D, int kRole>
+__global__ __launch_bounds__(kThreads, 1) void bwd_component_kernel(FusedArgs a) {
+    __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
+    FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
+    int g, pos;
+    job_of(a, g, pos);
+    const int QT = a.seqlen / 64;
+    if constexpr (kRole == 1) {
+        dkv_role<D, true, 1>(a, g, pos, pos, QT, -1, smem);
+    } else {
+        const int qt = QT - 1 - pos;
+        dq_role<D, true, 2>(a, g, qt, 0, qt + 1, -1, smem);
+    }
+}
+
 template <int D>
 void launch_d(const FusedArgs& a, bool causal) {
     const dim3 grid(a.n_groups * a.jobs_per_group);
@@ -892,7 +980,56 @@ void launch_d(const FusedArgs& a, bool causal) {
     else hipLaunchKernelGGL((bwd_fused_kernel<D, false>), grid, dim3(kThreads), 0, 0, a);
 }
 
+// XCD-aware job map: n_groups groups of jobs_per_group jobs.
+void set_job_map(FusedArgs& a) {
+    int gcd8 = 8;
+    while (a.n_groups % gcd8 != 0) gcd8 >>= 1;
+    const int parts = 8 / gcd8;  // smallest split with n_groups * parts % 8 == 0
+    const bool fits = a.jobs_per_group % parts == 0;
+    a.xcd_parts = fits ? parts : 0;
+    a.part_len = fits ? a.jobs_per_group / parts : 0;
+}
+
+FusedArgs base_args(const BwdProblem& p, const BwdTensors& t) {
+    FusedArgs a{};
+    a.q = (const _Float16*)t.q;
+    a.k = (const _Float16*)t.k;
+    a.v = (const _Float16*)t.v;
+    a.dout = (const _Float16*)t.dout;
+    a.dq = t.dq;
+    a.dk = t.dk;
+    a.dv = t.dv;
+    a.out_f32 = p.out_f32 ? 1 : 0;
+    a.seqlen = p.seqlen;
+    a.heads_q = p.heads_q;
+    a.heads_kv = p.heads_kv;
+    a.batch = p.batch;
+    a.n_groups = p.batch * p.heads_kv;
+    a.scale_log2 = p.scale * kLog2e;
+    a.scale = p.scale;
+    return a;
+}
+
 }  // namespace
+
+hipError_t launch_component(const BwdProblem& p, const BwdTensors& t, int role) {
+    FusedArgs a = base_args(p, t);
+    a.packed = t.packed_in;
+    a.smax = t.aux0;
+    a.ssum = t.aux1;
+    a.delta = t.delta_in;
+    a.jobs_per_group = p.seqlen / kTileN;
+    set_job_map(a);
+    const dim3 grid(a.n_groups * a.jobs_per_group);
+    if (p.head_dim == 128) {
+        if (role == 1) hipLaunchKernelGGL((bwd_component_kernel<128, 1>), grid, dim3(kThreads), 0, 0, a);
+        else hipLaunchKernelGGL((bwd_component_kernel<128, 2>), grid, dim3(kThreads), 0, 0, a);
+    } else {
+        if (role == 1) hipLaunchKernelGGL((bwd_component_kernel<64, 1>), grid, dim3(kThreads), 0, 0, a);
+        else hipLaunchKernelGGL((bwd_component_kernel<64, 2>), grid, dim3(kThreads), 0, 0, a);
+    }
+    return hipGetLastError();
+}
 
 hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace) {
     auto mark = [&](int i) {
@@ -906,36 +1043,18 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     int* counters = plan.bal_m > 0 ? reinterpret_cast<int*>(ws + plan.cnt_off) : nullptr;
 
     mark(0);
-    hipError_t err = launch_preprocess(p, t, lse2, ndelta, counters, plan.n_counters);
+    hipError_t err = t.packed_in != nullptr
+                         ? launch_rowstats(p, t, lse2, ndelta, counters, plan.n_counters)
+                         : launch_preprocess(p, t, lse2, ndelta, counters, plan.n_counters);
     if (err != hipSuccess) return err;
     mark(1);
 
-    FusedArgs a;
-    a.q = (const _Float16*)t.q;
-    a.k = (const _Float16*)t.k;
-    a.v = (const _Float16*)t.v;
-    a.dout = (const _Float16*)t.dout;
+    FusedArgs a = base_args(p, t);
     a.lse2 = lse2;
     a.ndelta = ndelta;
-    a.dq = (_Float16*)t.dq;
-    a.dk = (_Float16*)t.dk;
-    a.dv = (_Float16*)t.dv;
-    a.seqlen = p.seqlen;
-    a.heads_q = p.heads_q;
-    a.heads_kv = p.heads_kv;
-    a.batch = p.batch;
-    a.n_groups = p.batch * p.heads_kv;
-    a.jobs_per_group = (p.seqlen / kTileN) * (1 + p.heads_q / p.heads_kv);
-    {
-        int gcd8 = 8;
-        while (a.n_groups % gcd8 != 0) gcd8 >>= 1;
-        const int parts = 8 / gcd8;  // smallest split with n_groups * parts % 8 == 0
-        const bool fits = a.jobs_per_group % parts == 0;
-        a.xcd_parts = fits ? parts : 0;
-        a.part_len = fits ? a.jobs_per_group / parts : 0;
-    }
-    a.scale_log2 = p.scale * kLog2e;
-    a.scale = p.scale;
+    const int group = p.heads_q / p.heads_kv;
+    a.jobs_per_group = (p.seqlen / kTileN) * (1 + group);
+    set_job_map(a);
     a.bal_m = plan.bal_m;
     a.cnt_kv = 0;
     a.cnt_q = plan.n_counters / 2;
@@ -961,7 +1080,8 @@ WorkspacePlan plan_workspace(const BwdProblem& p) {
     // jobs (at most two per CU of an MI355X): see bwd_fused_kernel.
     const int qt = p.seqlen / kTileM;
     const long jobs = 2L * p.batch * p.heads_q * qt;
-    if (p.causal && p.heads_q == p.heads_kv && qt >= 4 && qt % 2 == 0 && jobs <= 512) {
+    if (p.causal && p.heads_q == p.heads_kv && qt >= 4 && qt % 2 == 0 &&
+        jobs <= 512) {
         w.bal_m = qt / 2;
         const size_t split_jobs = (size_t)p.batch * p.heads_q * w.bal_m;  // per role
         const size_t kv_piece = (size_t)4 * (p.head_dim / 64) * 2 * 16 * 64 * sizeof(float);

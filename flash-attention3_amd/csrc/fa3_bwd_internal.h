@@ -24,6 +24,7 @@ struct BwdProblem {
     bool causal = false;
     bool deterministic = false;
     float scale = 0.f;  // softmax scale
+    bool out_f32 = false;  // outputs fp32 (component entries) instead of fp16
 };
 
 struct BwdTensors {
@@ -40,6 +41,11 @@ struct BwdTensors {
     void* dv = nullptr;
     float* delta = nullptr;        // fp32 rows (softmax_d); may be null
     float* packed = nullptr;       // optional [rows][3] sidecar
+    // Row statistics given instead of computed from O (component entries):
+    // a packed [max_log2, inv_sum, delta] sidecar (fused5, dK/dV), or
+    // delta_in together with the raw max / sum pair in aux0 / aux1 (dQ).
+    const float* packed_in = nullptr;
+    const float* delta_in = nullptr;
     // Optional profiling events recorded on the null stream at the stage
     // boundaries: before preprocess, before main, before dQ finalize, after.
     hipEvent_t stage_events[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -75,5 +81,15 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
 // Alone, it is the component entry shaobo_fa3_bwd_dot_do_o.
 hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
                              float* ndelta, int* counters = nullptr, int n_counters = 0);
+
+// lse2 and -delta rows from the packed sidecar t.packed_in; also clears the
+// counters.
+hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta,
+                           int* counters, int n_counters);
+
+// Workspace-free single-role components (causal, heads_q == heads_kv, fp32
+// outputs when p.out_f32): role 1 writes dK / dV from t.packed_in, role 2
+// writes dQ from aux0 (raw max), aux1 (sum) and t.delta_in.
+hipError_t launch_component(const BwdProblem& p, const BwdTensors& t, int role);
 
 }  // namespace fa3

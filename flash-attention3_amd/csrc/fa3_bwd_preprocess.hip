@@ -88,7 +88,32 @@ hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, f
     return hipGetLastError();
 }
 
+// Row statistics from the packed sidecar [max_log2, inv_sum, delta]
+// (reference src/dot_do_o_kernel.cpp:49-61) for the fused5 entry:
+// lse2 = max_log2 - log2(inv_sum), since exp2(x - m) * inv = exp2(x - (m -
+// log2 inv)), and -delta.
+__global__ __launch_bounds__(256) void rowstats_kernel(const float* __restrict__ packed,
+                                                       float* __restrict__ lse2,
+                                                       float* __restrict__ ndelta,
+                                                       int* __restrict__ counters, int n_counters,
+                                                       int rows) {
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    if (r < n_counters) counters[r] = 0;
+    if (r >= rows) return;
+    lse2[r] = packed[(size_t)r * 3] - log2f(packed[(size_t)r * 3 + 1]);
+    ndelta[r] = -packed[(size_t)r * 3 + 2];
+}
+
 }  // namespace
+
+hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta,
+                           int* counters, int n_counters) {
+    const int rows = p.batch * p.heads_q * p.seqlen;
+    const int n = rows > n_counters ? rows : n_counters;
+    hipLaunchKernelGGL(rowstats_kernel, dim3((n + 255) / 256), dim3(256), 0, 0, t.packed_in,
+                       lse2, ndelta, counters, n_counters, rows);
+    return hipGetLastError();
+}
 
 hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
                              float* ndelta, int* counters, int n_counters) {

@@ -30,7 +30,15 @@ EXPORTS = (
     "shaobo_fa3_params_init", "shaobo_fa3_bwd_get_capabilities", "shaobo_fa3_bwd_v2_validate",
     "shaobo_fa3_bwd_v2_workspace_bytes", "shaobo_fa3_bwd_v2", "shaobo_fa3_status_string",
     "shaobo_fa3_bwd_workspace_bytes", "shaobo_fa3_bwd", "shaobo_fa3_bwd_dot_do_o",
+    "shaobo_fa3_bwd_fused5_workspace_bytes", "shaobo_fa3_bwd_fused5",
+    "shaobo_fa3_bwd_dkv_workspace_bytes", "shaobo_fa3_bwd_dkv",
+    "shaobo_fa3_bwd_dq_workspace_bytes", "shaobo_fa3_bwd_dq",
 )
+
+# Component path selectors (params.dkv_path / params.dq_path) of the canonical
+# dK/dV and dQ component kernels.
+DKV_PATH_CANONICAL = 5
+DQ_PATH_CANONICAL = 6
 
 
 class Params(ctypes.Structure):
@@ -124,6 +132,16 @@ def load(path=LIB_PATH):
         lib.shaobo_fa3_bwd.restype = ctypes.c_int
         lib.shaobo_fa3_bwd_dot_do_o.argtypes = [ctypes.c_void_p] * 6 + [ctypes.POINTER(Params)]
         lib.shaobo_fa3_bwd_dot_do_o.restype = ctypes.c_int
+        for name in ("fused5", "dkv", "dq"):
+            getattr(lib, f"shaobo_fa3_bwd_{name}_workspace_bytes").argtypes = [
+                ctypes.POINTER(Params)]
+            getattr(lib, f"shaobo_fa3_bwd_{name}_workspace_bytes").restype = ctypes.c_size_t
+        lib.shaobo_fa3_bwd_fused5.argtypes = [ctypes.c_void_p] * 8 + [ctypes.POINTER(Params)]
+        lib.shaobo_fa3_bwd_fused5.restype = ctypes.c_int
+        lib.shaobo_fa3_bwd_dkv.argtypes = [ctypes.c_void_p] * 10 + [ctypes.POINTER(Params)]
+        lib.shaobo_fa3_bwd_dkv.restype = ctypes.c_int
+        lib.shaobo_fa3_bwd_dq.argtypes = [ctypes.c_void_p] * 10 + [ctypes.POINTER(Params)]
+        lib.shaobo_fa3_bwd_dq.restype = ctypes.c_int
         if path != LIB_PATH:
             return lib
         _LIB = lib

@@ -28,6 +28,69 @@ int shaobo_fa3_bwd_dot_do_o(const void* dout,
                             void* packed_sidecar,
                             const ShaoboFa3Params* params);
 
+/* Fused backward from the packed sidecar (reference
+ * include/shaobo_fa3_components.h:47-58, src/fused_bwd_kernel.cpp:1673-1764):
+ * P = exp2(s * scale * log2 e - max_log2) * inv_sum, dS = P (dP - delta);
+ * dq, dk, dv fp16 BHSD.  softmax_scale is taken as given.  Accepts fp16 BHSD,
+ * Dqk == Dv in {64, 128}, causal 0/1, Sq == Sk with Sq % 128 == 0, Hq a
+ * multiple of Hkv (UNSUPPORTED otherwise); INVALID_VALUE for a null pointer
+ * or a workspace shorter than shaobo_fa3_bwd_fused5_workspace_bytes()
+ * (0 for an unsupported shape). */
+size_t shaobo_fa3_bwd_fused5_workspace_bytes(const ShaoboFa3Params* params);
+
+int shaobo_fa3_bwd_fused5(const void* dout,
+                          const void* q,
+                          const void* k,
+                          const void* v,
+                          const void* packed_sidecar,
+                          void* dq,
+                          void* dk,
+                          void* dv,
+                          const ShaoboFa3Params* params);
+
+/* dK / dV only, canonical path (params->dkv_path == 5; reference
+ * include/shaobo_fa3_components.h:10-22, src/dkv_kernel.cpp:1300-1421): the
+ * packed sidecar of shaobo_fa3_bwd_dot_do_o in params->reserved_ptr[3];
+ * dk, dv written as fp32 [B, H, S, D]; out, aux0, aux1 and dq are unused.
+ * One query head per KV head, causal, Sq == Sk, Sq % 128 == 0, fp16 BHSD,
+ * D in {64, 128}; other shapes and other dkv_path values are UNSUPPORTED
+ * (the reference's dkv_path 1 -- a naive kernel that recomputes the forward
+ * softmax from Q and K -- is not provided).  No workspace: the workspace-bytes
+ * query returns 0, as the reference's does for the canonical path. */
+size_t shaobo_fa3_bwd_dkv_workspace_bytes(const ShaoboFa3Params* params);
+
+int shaobo_fa3_bwd_dkv(const void* dout,
+                       const void* q,
+                       const void* k,
+                       const void* v,
+                       const void* out,
+                       const void* softmax_aux0,
+                       const void* softmax_aux1,
+                       void* dq,
+                       void* dk,
+                       void* dv,
+                       const ShaoboFa3Params* params);
+
+/* dQ only, canonical path (params->dq_path == 6; reference
+ * include/shaobo_fa3_components.h:24-36, src/dq_kernel.cpp:1497-1554):
+ * aux0 = raw row max, aux1 = row sum (SMAX_SSUM convention), delta in
+ * params->reserved_ptr[0]; dq written as fp32 [B, Hq, S, D]; out, dk, dv
+ * unused.  Shapes as for shaobo_fa3_bwd_dkv; dq_path 1 is not provided.
+ * No workspace (the workspace-bytes query returns 0). */
+size_t shaobo_fa3_bwd_dq_workspace_bytes(const ShaoboFa3Params* params);
+
+int shaobo_fa3_bwd_dq(const void* dout,
+                      const void* q,
+                      const void* k,
+                      const void* v,
+                      const void* out,
+                      const void* softmax_aux0,
+                      const void* softmax_aux1,
+                      void* dq,
+                      void* dk,
+                      void* dv,
+                      const ShaoboFa3Params* params);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -294,3 +294,81 @@ def test_validation_matches_reference_code(lib):
     lib.shaobo_fa3_params_init(ctypes.byref(a))
     ref.shaobo_fa3_params_init(ctypes.byref(b))
     assert bytes(a) == bytes(b)
+
+
+def component_params(lib, **kw):
+    p = F.make_params(lib, **{"batch": 1, "seqlen": 256, "heads_q": 2, "head_dim": 128,
+                              "causal": True, "softmax_scale": 0.125, **kw})
+    p.dkv_path = F.DKV_PATH_CANONICAL
+    p.dq_path = F.DQ_PATH_CANONICAL
+    return p
+
+
+def test_component_workspace_sizes(lib):
+    """dkv / dq need no workspace (as the reference's canonical paths,
+    src/dkv_kernel.cpp:1289-1298, src/dq_kernel.cpp:1486-1495); fused5 needs
+    the v2 plan's rows (and split buffers), 0 for an unsupported shape."""
+    for f in ("dkv", "dq"):
+        fn = getattr(lib, f"shaobo_fa3_bwd_{f}_workspace_bytes")
+        assert fn(ctypes.byref(component_params(lib))) == 0
+        assert fn(None) == 0
+    ws5 = lib.shaobo_fa3_bwd_fused5_workspace_bytes
+    assert ws5(None) == 0
+    assert ws5(ctypes.byref(component_params(lib, seqlen=2048, heads_q=4))) == \
+        split_plan_bytes(1, 4, 2048, 128)
+    p = component_params(lib, heads_q=4, heads_kv=2, causal=False)
+    assert ws5(ctypes.byref(p)) == 2 * 4 * 256 * 4
+    p = component_params(lib)
+    p.seqlen_k = 512
+    assert ws5(ctypes.byref(p)) == 0
+    p = component_params(lib, head_dim=96)
+    assert ws5(ctypes.byref(p)) == 0
+
+
+def test_component_error_paths_without_gpu(lib):
+    """Shape / path checks come before pointer checks, as in the reference
+    (src/dkv_kernel.cpp:1390-1398, src/dq_kernel.cpp:1515-1525,
+    src/fused_bwd_kernel.cpp:1682-1703); every case returns before a launch."""
+    one = ctypes.c_void_p(16)
+    ten = [one] * 10
+    for name, mut in [("dkv_path", 1), ("causal", 0), ("num_heads_kv", 1), ("head_dim_qk", 96),
+                      ("seqlen_q", 200), ("dtype", F.DTYPE_BF16), ("layout", F.LAYOUT_BSHD)]:
+        p = component_params(lib)
+        p.reserved_ptr[3] = 16
+        setattr(p, name, mut)
+        assert lib.shaobo_fa3_bwd_dkv(*ten, ctypes.byref(p)) == F.UNSUPPORTED, name
+    for name, mut in [("dq_path", 1), ("dq_path", 5), ("causal", 0), ("seqlen_k", 512)]:
+        p = component_params(lib)
+        p.reserved_ptr[0] = 16
+        setattr(p, name, mut)
+        assert lib.shaobo_fa3_bwd_dq(*ten, ctypes.byref(p)) == F.UNSUPPORTED, name
+    assert lib.shaobo_fa3_bwd_dkv(*ten, None) == F.INVALID_VALUE
+    assert lib.shaobo_fa3_bwd_dq(*ten, None) == F.INVALID_VALUE
+    p = component_params(lib)  # sidecar missing in reserved_ptr[3]
+    assert lib.shaobo_fa3_bwd_dkv(*ten, ctypes.byref(p)) == F.INVALID_VALUE
+    p.reserved_ptr[3] = 16
+    bad = list(ten)
+    bad[8] = None  # dk
+    assert lib.shaobo_fa3_bwd_dkv(*bad, ctypes.byref(p)) == F.INVALID_VALUE
+    p = component_params(lib)  # delta missing in reserved_ptr[0]
+    assert lib.shaobo_fa3_bwd_dq(*ten, ctypes.byref(p)) == F.INVALID_VALUE
+    p.reserved_ptr[0] = 16
+    bad = list(ten)
+    bad[6] = None  # aux1 (row sum)
+    assert lib.shaobo_fa3_bwd_dq(*bad, ctypes.byref(p)) == F.INVALID_VALUE
+    # fused5
+    eight = [one] * 8
+    p = component_params(lib, heads_q=3, heads_kv=2)
+    assert lib.shaobo_fa3_bwd_fused5(*eight, ctypes.byref(p)) == F.UNSUPPORTED
+    p = component_params(lib)
+    p.causal = 2
+    assert lib.shaobo_fa3_bwd_fused5(*eight, ctypes.byref(p)) == F.UNSUPPORTED
+    p = component_params(lib)
+    bad = list(eight)
+    bad[4] = None  # packed sidecar
+    assert lib.shaobo_fa3_bwd_fused5(*bad, ctypes.byref(p)) == F.INVALID_VALUE
+    p.workspace, p.workspace_bytes = 16, 8  # too small
+    assert lib.shaobo_fa3_bwd_fused5(*eight, ctypes.byref(p)) == F.INVALID_VALUE
+    p.workspace, p.workspace_bytes = None, 1 << 30
+    assert lib.shaobo_fa3_bwd_fused5(*eight, ctypes.byref(p)) == F.INVALID_VALUE
+    assert lib.shaobo_fa3_bwd_fused5(*eight, None) == F.INVALID_VALUE
