@@ -3,10 +3,10 @@
 // src/fused_bwd_dq_reduce.cpp:27-109, and the legacy dKV / dQ kernels
 // src/dkv_kernel.cpp:957-1085, src/dq_kernel.cpp:794-953).  It runs after the
 // delta preprocess (fa3_bwd_preprocess.hip), which supplies per query row
-// delta = rowsum(dO * O) and lse2 = LSE * log2(e).
+// lse2 = LSE * log2(e) and -delta = -rowsum(dO * O); the component kernels at
+// the end of this file read the reference's row statistics directly instead.
 //
-// Two workgroup roles share one grid, and no workgroup ever adds into memory
-// another one writes (no atomics, no partial buffers, bitwise deterministic):
+// Two job roles; each output element has one writer:
 //
 //  * dKV role -- owns a 64-key tile of one KV head; streams every 64-row query
 //    tile that can see it (causal: from the diagonal on) of every query head
@@ -19,24 +19,31 @@
 //
 // The softmax scale is folded out of dS and applied once to dK and dQ.
 //
-// Each workgroup has 8 waves, two per SIMD, so one wave's MFMAs overlap the
-// other's softmax, LDS traffic and waits.  A pipeline step has two phases:
-//   phase 1: the 64 x 64 score and dP tiles in 16 x 16 blocks
-//            (v_mfma_f32_16x16x32_f16); each wave owns 16 x 32 of them and
-//            turns them into P / dS (fp16), which it writes to LDS;
-//   phase 2: the output products with v_mfma_f32_32x32x16_f16; each wave owns
-//            a 32-wide slice of D (and, where there are more waves than
-//            slices, part of the contraction, added through LDS at the end),
-//            reading P / dS from LDS; its other operand (the streamed tile,
-//            transposed by ds_read_b64_tr_b16) is read one step earlier, in
-//            phase 1 of that tile, and carried in registers.
-// Step j runs phase 1 of tile j + 1 and phase 2 of tile j, so P / dS are
-// double-buffered and one barrier per step suffices.  Every global read of
-// the loop is a direct-to-LDS load (global_load_lds) into one of three
-// stages, issued two steps ahead: a stage holds a streamed tile pair and, in
-// the dKV role, its 64 lse2 / delta values.  The issue pattern is the same
-// every step (a finished stream re-loads its last tile into a free stage), so
-// every wait is a constant count.
+// A workgroup runs one job with 8 waves, two per SIMD, specialised:
+//   score waves 0..3: S and dP of 16 rows x 64 columns of the step's tile
+//            pair (v_mfma_f32_16x16x32_f16; -delta seeds the dP
+//            accumulators), then P and dS in fp16 into LDS;
+//   gradient waves 4..7: the output products (v_mfma_f32_32x32x16_f16) over
+//            the P / dS written one step earlier, each wave a share of the
+//            (matrix, 32-wide D slice) pairs; the streamed tile's transposed
+//            operand (ds_read_b64_tr_b16) is read one step ahead and carried
+//            in registers.
+// In step j the score waves make P / dS of tile j + 1 while the gradient
+// waves consume those of tile j, so P / dS are double-buffered and one
+// barrier per step suffices; both loops pass the same barriers, and the
+// compiler allocates registers for the larger of the two, not their sum.
+// Every global read of the loop is a direct-to-LDS load (global_load_lds)
+// into one of three stages, issued two steps ahead: a stage holds a streamed
+// tile pair and, in the dKV role, its 64 rows' statistics.  The issue pattern
+// is the same every step (a finished stream re-loads its last tile into a
+// free stage), so every wait is a constant count.
+//
+// Split plan (causal, one query head per KV head, at most 512 jobs; see
+// bwd_fused_kernel): long jobs are cut in two pieces run by different
+// workgroups.  Each piece stores its fp32 partial sums with device-coherent
+// stores and then bumps an arrival counter; the piece that arrives second
+// adds piece 0 + piece 1 in that fixed order and writes the output, so the
+// result does not depend on which piece finished first.
 #include "fa3_bwd_device.h"
 #include "fa3_bwd_internal.h"
 
