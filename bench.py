@@ -140,7 +140,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warm-up steps (default: at least 20, and enough for "
+                         "0.2 s of GPU work, which brings the clocks to their steady state)")
     ap.add_argument("--config", default="P3", choices=sorted(CONFIGS))
     ap.add_argument("--deterministic", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
@@ -179,9 +181,20 @@ def main():
         if st != F.SUCCESS:
             raise RuntimeError("shaobo_fa3_bwd_v2: " + F.status_name(st))
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    if args.warmup is not None:
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+    else:
+        # The GPU's clocks ramp up over tens of milliseconds of sustained work:
+        # warm up for at least 0.2 s (and 20 steps), in batches of 20.
+        args.warmup = 0
+        t_w = time.perf_counter()
+        while args.warmup < 20 or time.perf_counter() - t_w < 0.2:
+            for _ in range(20):
+                step()
+            args.warmup += 20
+            torch.cuda.synchronize()
 
     # ---- timed region: exactly `steps` backward lifecycles ----
     e0, e1 = hip.event(), hip.event()

@@ -118,12 +118,12 @@ struct Cfg {
     static constexpr int kStepsQ = 4 / kSplitQ;
     static constexpr int kPdsBytes = 64 * 64 * 2;           // one [64][64] fp16 tile
     static constexpr int kPdsOff = kStages * kStageBytes;   // P / dS double buffer
-    static constexpr int kBytes = kPdsOff + 2 * 2 * kPdsBytes;
+    static constexpr int kFlagOff = kPdsOff + 2 * 2 * kPdsBytes;  // split-plan flag word
+    static constexpr int kBytes = kFlagOff + 256;
     static_assert(kLoadsPerTile >= 1, "tile covers all waves");
     static_assert(kStageBytes % 512 == 0 && kPdsOff % 512 == 0, "bank-aligned tiles");
     static_assert(2 * kTileBytes <= 2 * 2 * kPdsBytes, "prologue staging fits the P / dS area");
     static_assert(kBytes <= 160 * 1024, "LDS budget");
-    static_assert(kWaves * 2 * 16 * 64 * 4 <= kBytes, "epilogue exchange fits");
 };
 
 // s_waitcnt vmcnt(N) lgkmcnt(0): all but the last N vector-memory loads have
@@ -211,6 +211,17 @@ __device__ __forceinline__ void load_rows_async(FA3_LDS char* rows, const FusedA
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Wave issue priority, pinned in program order.  A score wave runs its LDS
+// reads and S / dP MFMAs at raised priority: its MFMAs then win the SIMD's
+// matrix unit over the gradient wave's, so its softmax and P / dS writes
+// (VALU, LDS) run beside the gradient wave's MFMAs instead of after them.
+template <int kPrio>
+__device__ __forceinline__ void set_prio() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(kPrio);
+    __builtin_amdgcn_sched_barrier(0);
+}
 
 // A operand (32 x 16: m = D column, k = tile row) of a phase-2 product, read
 // transposed from a swizzled [64][D] tile: lane l gets column 32 db + l % 32,
@@ -320,25 +331,40 @@ __device__ __forceinline__ float get_partial(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// End of one piece of a split job, after its partial sums are stored: wait
-// until every wave's partial stores have completed, count the arrival, and
-// return true in every wave of the workgroup that arrives second; that one
-// reads both pieces (after its counter update, so it sees the other piece's
-// completed stores) and adds them in a fixed order, so the result does not
-// depend on which piece arrives last.  The counter was cleared by the
-// preprocess; the last arriver clears it again.
-__device__ __forceinline__ bool finish_split(int* counter, FA3_LDS char* smem) {
+// End of one piece of a split job.  Every wave of the workgroup calls it
+// after its last pipeline step -- the gradient waves with put_own storing
+// their partial sums, the score waves with a no-op -- and it returns true in
+// every wave when this workgroup is to write the job's output.
+//
+// Score wave 0 has already peeked at the job's arrival counter into *flag
+// (right after its last barrier, while the gradient waves ran the last
+// products).  If the other piece had arrived, its partial sums are complete
+// and visible, so this piece adds them to its registers and needs no partial
+// of its own.  Otherwise it stores its partial sums, waits until every wave's
+// stores have completed, and counts its arrival; the piece that arrives
+// second then adds the other piece's partial sums.  Either way the output is
+// piece 0 + piece 1 (a two-term sum is the same in either order), so the
+// result does not depend on which piece finishes first.  The counters are
+// cleared by the preprocess kernel before every launch.
+template <typename PutOwn>
+__device__ __forceinline__ bool split_end(int* counter, FA3_LDS int* flag, PutOwn&& put_own) {
     wait_vm_lgkm0<0>();
     barrier();
-    FA3_LDS int* flag = (FA3_LDS int*)smem;
-    if (threadIdx.x == 0) {
-        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = old;
-    }
+    if (*flag == 1) return true;
+    put_own();
+    wait_vm_lgkm0<0>();
+    barrier();
+    if (threadIdx.x == 0)
+        *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wait_vm_lgkm0<0>();
     barrier();
     return *flag == 1;
+}
+
+__device__ __forceinline__ void split_peek(const int* counter, FA3_LDS int* flag) {
+    if (threadIdx.x == 0)
+        *flag = __hip_atomic_load(const_cast<int*>(counter), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ----------------------------------------------------------------------------
@@ -346,7 +372,7 @@ __device__ __forceinline__ bool finish_split(int* counter, FA3_LDS char* smem) {
 // ----------------------------------------------------------------------------
 // Streams query tiles [qa, qb) of every query head of the group.  slot < 0:
 // the job is whole and writes dK / dV; otherwise the unit is piece slot & 1
-// of split job slot >> 1 and the pieces' partial sums meet in finish_split.
+// of split job slot >> 1 and the pieces' partial sums meet in split_end.
 template <int D, bool kCausal, int kRows = 0>
 __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, int slot,
                          FA3_LDS char* smem) {
@@ -400,6 +426,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         st_2 = x;
     };
     FA3_LDS char* pds0 = smem + C::kPdsOff;
+    FA3_LDS int* flag = (FA3_LDS int*)(smem + C::kFlagOff);
     FA3_LDS char* pds1 = pds0 + 2 * C::kPdsBytes;
     auto prologue_loads = [&]() {
         // this key tile's K and V are staged in the P / dS area
@@ -429,6 +456,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         // transposed ([key][row]) into the P / dS buffer
         auto score = [&](bool masked, const FA3_LDS char* st, FA3_LDS char* pds) {
             f16x8 aq[C::kKs], ad[C::kKs];
+            set_prio<3>();
 #pragma unroll
             for (int s = 0; s < C::kKs; ++s) {
                 const uint32_t off = tile_off<D>(16 * t + l16, p1_chunk<D>(s, g4));
@@ -461,6 +489,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                     pacc[kb] = mfma_16x16x32(ad[s], vf[kb][s], s == 0 ? ndl : pacc[kb]);
                 }
             }
+            set_prio<0>();
             float p[16], ds[16];
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
@@ -526,6 +555,11 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         }
         if (j + 1 < n_it) step(st_ld, st_1, pds1);
         top();  // matches the gradient waves' last phase
+        if (slot >= 0) {
+            int* counter = a.counters + a.cnt_kv + (slot >> 1);
+            split_peek(counter, flag);
+            split_end(counter, flag, [] {});
+        }
     } else {
         // ---- gradient waves: dV^T and dK^T for D slice(s); wave t owns the
         // (matrix, slice) pairs u = kPpw t .. +kPpw, matrix = u % 2 (0: dV
@@ -607,34 +641,32 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         }
         if (slot < 0) {
             store_dkv<D>(a, bkv, kbase, t, lane, acc);
-        } else {
-            // partial sums in register order: [wave][register][lane]
-            float* pp = a.part_kv + ((size_t)slot * 4 + t) * (kPpw * 2 * 16 * 64) + lane;
-#pragma unroll
-            for (int u = 0; u < kPpw; ++u)
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) put_partial(&pp[((u * 2 + kb) * 16 + i) * 64], acc[u][kb][i]);
+            return;
         }
-    }
-    if (slot >= 0 && finish_split(a.counters + a.cnt_kv + (slot >> 1), smem)) {
-        if (w >= 4) {
-            // last piece of the job: dK / dV = piece 0 + piece 1
-            constexpr int kPpw = C::kDB / 2;
-            constexpr int kRegs = kPpw * 2 * 16;
-            const float* p0 = a.part_kv + ((size_t)(slot & ~1) * 4 + t) * (kRegs * 64) + lane;
-            const float* p1 = p0 + (size_t)4 * kRegs * 64;
-            f32x16 acc[kPpw][2];
+        // partial sums in register order: [piece][wave][register][lane]
+        constexpr int kRegs = kPpw * 2 * 16;
+        auto part = [&](int piece) {
+            return a.part_kv + ((size_t)piece * 4 + t) * (kRegs * 64) + lane;
+        };
+        auto put_own = [&] {
+            float* pp = part(slot);
 #pragma unroll
             for (int u = 0; u < kPpw; ++u)
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int r = ((u * 2 + kb) * 16 + i) * 64;
-                        acc[u][kb][i] = get_partial(p0 + r) + get_partial(p1 + r);
-                    }
+                    for (int i = 0; i < 16; ++i)
+                        put_partial(&pp[((u * 2 + kb) * 16 + i) * 64], acc[u][kb][i]);
+        };
+        if (split_end(a.counters + a.cnt_kv + (slot >> 1), flag, put_own)) {
+            const float* po = part(slot ^ 1);
+#pragma unroll
+            for (int u = 0; u < kPpw; ++u)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        acc[u][kb][i] += get_partial(po + ((u * 2 + kb) * 16 + i) * 64);
             store_dkv<D>(a, bkv, kbase, t, lane, acc);
         }
     }
@@ -689,6 +721,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         st_2 = x;
     };
     FA3_LDS char* ds0 = smem + C::kPdsOff;
+    FA3_LDS int* flag = (FA3_LDS int*)(smem + C::kFlagOff);
     FA3_LDS char* ds1 = ds0 + 2 * C::kPdsBytes;
     auto prologue_loads = [&]() {
         // this query tile's Q and dO are staged in the dS area, its lse2 and
@@ -713,6 +746,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         f32x4 sacc[4], pacc[4];  // keys 16 t + 4 g4 + i, rows 16 rb + l16
         auto score = [&](bool masked, const FA3_LDS char* st, FA3_LDS char* ds) {
             f16x8 ak[C::kKs], av[C::kKs];
+            set_prio<3>();
 #pragma unroll
             for (int s = 0; s < C::kKs; ++s) {
                 const uint32_t off = tile_off<D>(16 * t + l16, p1_chunk<D>(s, g4));
@@ -727,6 +761,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
                     pacc[rb] = mfma_16x16x32(av[s], df[rb][s], s == 0 ? ndl[rb] : pacc[rb]);
                 }
             }
+            set_prio<0>();
             float p[16];
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
@@ -792,6 +827,11 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         }
         if (j + 1 < n_kt) step(kCausal && ka + j + 1 == qt, st_ld, st_1, ds1);
         top();  // matches the gradient waves' last phase
+        if (slot >= 0) {
+            int* counter = a.counters + a.cnt_q + (slot >> 1);
+            split_peek(counter, flag);
+            split_end(counter, flag, [] {});
+        }
     } else {
         // ---- gradient waves: dQ^T slice(s) over query rows; D = 128: slice
         // t, both 32-row blocks; D = 64: slice t / 2, row block t % 2
@@ -855,27 +895,41 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         }
         if (slot < 0) {
             store_dq<D>(a, row0, t, lane, acc);
-        } else {
-            float* pp = a.part_q + ((size_t)slot * 4 + t) * (kRb * 16 * 64) + lane;
+            return;
+        }
+        auto part = [&](int piece) {
+            return a.part_q + ((size_t)piece * 4 + t) * (kRb * 16 * 64) + lane;
+        };
+        auto put_own = [&] {
+            float* pp = part(slot);
 #pragma unroll
             for (int r = 0; r < kRb; ++r)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) put_partial(&pp[(r * 16 + i) * 64], acc[r][i]);
-        }
-    }
-    if (slot >= 0 && finish_split(a.counters + a.cnt_q + (slot >> 1), smem)) {
-        if (w >= 4) {
-            constexpr int kRb = C::kDB / 2;
-            const float* p0 = a.part_q + ((size_t)(slot & ~1) * 4 + t) * (kRb * 16 * 64) + lane;
-            const float* p1 = p0 + (size_t)4 * kRb * 16 * 64;
-            f32x16 acc[kRb];
+        };
+        if (split_end(a.counters + a.cnt_q + (slot >> 1), flag, put_own)) {
+            const float* po = part(slot ^ 1);
 #pragma unroll
             for (int r = 0; r < kRb; ++r)
 #pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    acc[r][i] = get_partial(p0 + (r * 16 + i) * 64) + get_partial(p1 + (r * 16 + i) * 64);
+                for (int i = 0; i < 16; ++i) acc[r][i] += get_partial(po + (r * 16 + i) * 64);
             store_dq<D>(a, row0, t, lane, acc);
         }
+    }
+}
+
+// Block id -> (group, position in the group); see the job map below.
+__device__ __forceinline__ void job_of(const FusedArgs& a, int& g, int& pos) {
+    const int id = blockIdx.x;
+    if (a.xcd_parts > 0) {
+        const int xcd = id & 7;
+        const int n = id >> 3;
+        const int v = xcd + 8 * (n / a.part_len);  // virtual group = (group, part)
+        g = v / a.xcd_parts;
+        pos = v % a.xcd_parts + a.xcd_parts * (n % a.part_len);
+    } else {
+        g = id / a.jobs_per_group;
+        pos = id % a.jobs_per_group;
     }
 }
 
@@ -903,20 +957,6 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
 //                   p - 2M .. p - M - 1);
 //   p in [3M, 4M):  dQ head piece of query tile p - 2M (key tiles 0 .. M - 1).
 // Every workgroup runs M or M + 1 steps.
-__device__ __forceinline__ void job_of(const FusedArgs& a, int& g, int& pos) {
-    const int id = blockIdx.x;
-    if (a.xcd_parts > 0) {
-        const int xcd = id & 7;
-        const int n = id >> 3;
-        const int v = xcd + 8 * (n / a.part_len);  // virtual group = (group, part)
-        g = v / a.xcd_parts;
-        pos = v % a.xcd_parts + a.xcd_parts * (n % a.part_len);
-    } else {
-        g = id / a.jobs_per_group;
-        pos = id % a.jobs_per_group;
-    }
-}
-
 template <int D, bool kCausal>
 __global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
