@@ -88,8 +88,10 @@ struct FusedArgs {
     int cnt_kv;        // offset of the split dKV jobs' counters in `counters`
     int cnt_q;         // offset of the split dQ jobs' counters
     int* counters;
-    float* part_kv;    // [job][piece][wave][register][lane] fp32
+    float* part_kv;    // [job][piece][wave][register / 4][lane][4] fp32
     float* part_q;
+    uint32_t part_kv_bytes;
+    uint32_t part_q_bytes;
 };
 
 constexpr int kWaves = 8;
@@ -321,14 +323,50 @@ __device__ __forceinline__ void store_dq(const FusedArgs& a, size_t row0, int t,
 
 // Partial sums of split jobs travel between workgroups (possibly on
 // different XCDs, whose L2 caches are not coherent with each other) through
-// agent-scope atomic stores and loads: those are coherent device-wide by
-// themselves, so no cache-wide writeback / invalidate (which would also
-// evict the tiles every CU of the XCD is streaming) is needed.
-__device__ __forceinline__ void put_partial(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// 16-byte buffer loads and stores with the sc1 cache policy -- the policy
+// this chip's agent-scope atomic loads and stores use, coherent device-wide
+// by itself -- so no cache-wide writeback / invalidate (which would also
+// evict the tiles every CU of the XCD is streaming) is needed.  A wave's
+// accumulators go out as [register / 4][lane][4]: one instruction moves 1 KiB
+// of consecutive bytes.
+constexpr int kCachePolicySc1 = 16;
+constexpr int kBufferWord3 = 0x00020000;  // raw 32-bit buffer access on gfx9
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(float* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, kBufferWord3);
 }
-__device__ __forceinline__ float get_partial(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+// Stores / adds the N accumulator blocks of one wave at byte offset base.
+template <int N>
+__device__ __forceinline__ void put_partials(__amdgpu_buffer_rsrc_t r, uint32_t base,
+                                             const f32x16* acc, int lane) {
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 v = {acc[n][4 * g], acc[n][4 * g + 1], acc[n][4 * g + 2], acc[n][4 * g + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r,
+                                                   base + ((n * 4 + g) * 64 + lane) * 16, 0,
+                                                   kCachePolicySc1);
+        }
+}
+template <int N>
+__device__ __forceinline__ void add_partials(__amdgpu_buffer_rsrc_t r, uint32_t base, f32x16* acc,
+                                             int lane) {
+    f32x4 v[N][4];
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            v[n][g] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           r, base + ((n * 4 + g) * 64 + lane) * 16, 0, kCachePolicySc1));
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[n][4 * g + e] += v[n][g][e];
 }
 
 // End of one piece of a split job.  Every wave of the workgroup calls it
@@ -643,30 +681,14 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
             store_dkv<D>(a, bkv, kbase, t, lane, acc);
             return;
         }
-        // partial sums in register order: [piece][wave][register][lane]
-        constexpr int kRegs = kPpw * 2 * 16;
-        auto part = [&](int piece) {
-            return a.part_kv + ((size_t)piece * 4 + t) * (kRegs * 64) + lane;
-        };
-        auto put_own = [&] {
-            float* pp = part(slot);
-#pragma unroll
-            for (int u = 0; u < kPpw; ++u)
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i)
-                        put_partial(&pp[((u * 2 + kb) * 16 + i) * 64], acc[u][kb][i]);
-        };
-        if (split_end(a.counters + a.cnt_kv + (slot >> 1), flag, put_own)) {
-            const float* po = part(slot ^ 1);
-#pragma unroll
-            for (int u = 0; u < kPpw; ++u)
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i)
-                        acc[u][kb][i] += get_partial(po + ((u * 2 + kb) * 16 + i) * 64);
+        // partial sums: [piece][wave][2 kPpw accumulator blocks]
+        constexpr int kBlk = 2 * kPpw;
+        const __amdgpu_buffer_rsrc_t pr = partial_rsrc(a.part_kv, a.part_kv_bytes);
+        auto part = [&](int piece) { return (uint32_t)(piece * 4 + t) * (kBlk * 4096); };
+        f32x16* flat = &acc[0][0];
+        if (split_end(a.counters + a.cnt_kv + (slot >> 1), flag,
+                      [&] { put_partials<kBlk>(pr, part(slot), flat, lane); })) {
+            add_partials<kBlk>(pr, part(slot ^ 1), flat, lane);
             store_dkv<D>(a, bkv, kbase, t, lane, acc);
         }
     }
@@ -897,22 +919,12 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
             store_dq<D>(a, row0, t, lane, acc);
             return;
         }
-        auto part = [&](int piece) {
-            return a.part_q + ((size_t)piece * 4 + t) * (kRb * 16 * 64) + lane;
-        };
-        auto put_own = [&] {
-            float* pp = part(slot);
-#pragma unroll
-            for (int r = 0; r < kRb; ++r)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) put_partial(&pp[(r * 16 + i) * 64], acc[r][i]);
-        };
-        if (split_end(a.counters + a.cnt_q + (slot >> 1), flag, put_own)) {
-            const float* po = part(slot ^ 1);
-#pragma unroll
-            for (int r = 0; r < kRb; ++r)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[r][i] += get_partial(po + (r * 16 + i) * 64);
+        // partial sums: [piece][wave][kRb accumulator blocks]
+        const __amdgpu_buffer_rsrc_t pr = partial_rsrc(a.part_q, a.part_q_bytes);
+        auto part = [&](int piece) { return (uint32_t)(piece * 4 + t) * (kRb * 4096); };
+        if (split_end(a.counters + a.cnt_q + (slot >> 1), flag,
+                      [&] { put_partials<kRb>(pr, part(slot), acc, lane); })) {
+            add_partials<kRb>(pr, part(slot ^ 1), acc, lane);
             store_dq<D>(a, row0, t, lane, acc);
         }
     }
@@ -1108,6 +1120,8 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     a.counters = counters;
     a.part_kv = plan.bal_m > 0 ? reinterpret_cast<float*>(ws + plan.pkv_off) : nullptr;
     a.part_q = plan.bal_m > 0 ? reinterpret_cast<float*>(ws + plan.pq_off) : nullptr;
+    a.part_kv_bytes = (uint32_t)(plan.pq_off - plan.pkv_off);
+    a.part_q_bytes = (uint32_t)(plan.total - plan.pq_off);
     if (p.head_dim == 128) launch_d<128>(a, p.causal);
     else launch_d<64>(a, p.causal);
     err = hipGetLastError();
