@@ -113,10 +113,11 @@ def backward(q, k, v, out, dout, smax, ssum, causal, scale, bkv=None, threads=No
     return delta, dq, dk, dv
 
 
-def golden(B, Hq, Hkv, S, D, causal, scale=None, kind="randn", bkv=None, threads=None):
+def golden(B, Hq, Hkv, S, D, causal, scale=None, kind="randn", bkv=None, threads=None,
+           seed_offset=0):
     """Inputs + forward + backward in one call (dict of numpy arrays)."""
     scale = 1.0 / math.sqrt(D) if scale is None else scale
-    x = make_inputs(B, Hq, Hkv, S, D, kind)
+    x = make_inputs(B, Hq, Hkv, S, D, kind, seed_offset)
     out, smax, ssum, lse = forward(x["q"], x["k"], x["v"], causal, scale, bkv, threads)
     delta, dq, dk, dv = backward(x["q"], x["k"], x["v"], out, x["dout"], smax, ssum, causal,
                                  scale, bkv, threads)

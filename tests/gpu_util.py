@@ -19,7 +19,7 @@ def dev(t, torch):
 
 
 def run_v2(g, torch, *, deterministic=False, with_softmax_d=True, lse=None, scale_is_set=True,
-           workspace_pad=0):
+           workspace_pad=0, workspace=None):
     """Run shaobo_fa3_bwd_v2 on the oracle's inputs; returns numpy fp32
     (delta, dq, dk, dv) and the status."""
     lib = F.load()
@@ -32,9 +32,13 @@ def run_v2(g, torch, *, deterministic=False, with_softmax_d=True, lse=None, scal
                       deterministic=deterministic, sync=True)
     nbytes = lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
     assert nbytes > 0
-    ws = torch.empty(nbytes + workspace_pad, dtype=torch.uint8, device="cuda")
-    # poison the workspace: the library must not rely on its contents
-    ws.fill_(0xC3)
+    if workspace is None:
+        ws = torch.empty(nbytes + workspace_pad, dtype=torch.uint8, device="cuda")
+        # poison the workspace: the library must not rely on its contents
+        ws.fill_(0xC3)
+    else:
+        ws = workspace
+        assert ws.numel() >= nbytes
     p.workspace = ws.data_ptr()
     p.workspace_bytes = ws.numel()
     dq = torch.full_like(q, float("nan"))

@@ -86,6 +86,26 @@ def test_deterministic_mode_is_bitwise_repeatable(hq, hkv, s, d):
         np.testing.assert_array_equal(r1[n], r2[n])
 
 
+@pytest.mark.parametrize("hq,s,d", [(2, 1024, 128), (4, 2048, 128), (2, 512, 64)])
+def test_split_plan_reused_workspace(hq, s, d):
+    """Split plan, one workspace kept across calls on different inputs: the
+    partial sums and arrival counters of one call must never leak into the
+    next (counters are cleared per call; partial sums are read only after the
+    other piece of the same call has written them)."""
+    log(f"[case] split plan reused workspace Hq{hq} S{s} D{d}")
+    ws = None
+    for seed in range(3):
+        g = O.golden(1, hq, hq, s, d, True, seed_offset=101 * seed)
+        if ws is None:
+            lib = F.load()
+            p = F.make_params(lib, batch=1, seqlen=s, heads_q=hq, head_dim=d, causal=True)
+            ws = torch.empty(lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p)),
+                             dtype=torch.uint8, device="cuda")
+        res = run_v2(g, torch, workspace=ws)
+        assert res["status"] == F.SUCCESS
+        check(res, g)
+
+
 def test_default_scale_and_internal_delta():
     """softmax_scale_is_set = 0 -> 1/sqrt(D); softmax_d = NULL keeps delta internal."""
     log("[case] default scale, softmax_d NULL")
