@@ -275,6 +275,15 @@ __device__ __forceinline__ void store4(const FusedArgs& a, void* base, size_t of
 // dV^T / dK^T accumulators of gradient wave t (pairs kPpw t .. +kPpw, pair =
 // 2 db + matrix) to dV / dK; lane: key 32 kb + l32,
 // d = 32 db + 8 (i / 4) + 4 h + i % 4.
+// (matrix, D slice) pair u of dKV gradient wave t, as pu = 2 slice + matrix
+// (matrix 0: dV from dO and P, 1: dK from Q and dS).  Waves 0, 1 own dV and
+// waves 2, 3 own dK, each for D / 64 consecutive 32-wide slices, so a wave
+// reads only one of the P / dS tiles.
+template <int D>
+__device__ __forceinline__ int dkv_pair(int t, int u) {
+    return 2 * ((D / 64) * (t & 1) + u) + (t >> 1);
+}
+
 template <int D>
 __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase, int t, int lane,
                                           const f32x16 (&acc)[D / 64][2]) {
@@ -282,7 +291,7 @@ __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase
     const int l32 = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int u = 0; u < kPpw; ++u) {
-        const int pu = kPpw * t + u;
+        const int pu = dkv_pair<D>(t, u);
         const float mul = (pu & 1) == 0 ? 1.f : a.scale;
         void* outp = (pu & 1) == 0 ? a.dv : a.dk;
         const size_t off0 = ((size_t)bkv * a.seqlen + kbase) * D + 32 * (pu >> 1) + 4 * h;
@@ -600,9 +609,8 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         }
     } else {
         // ---- gradient waves: dV^T and dK^T for D slice(s); wave t owns the
-        // (matrix, slice) pairs u = kPpw t .. +kPpw, matrix = u % 2 (0: dV
-        // from dO and P, 1: dK from Q and dS), slice db = u / 2, over all 64
-        // keys (two 32-key blocks)
+        // (matrix, slice) pairs dkv_pair(t, 0 .. kPpw - 1) over all 64 keys
+        // (two 32-key blocks)
         constexpr int kPpw = C::kDB / 2;
         f32x16 acc[kPpw][2];
 #pragma unroll
@@ -615,25 +623,25 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         auto read_xt = [&](const FA3_LDS char* st, f16x8 (&xt)[kPpw][4]) {
 #pragma unroll
             for (int u = 0; u < kPpw; ++u) {
-                const int pu = kPpw * t + u;
+                const int pu = dkv_pair<D>(t, u);
                 const FA3_LDS char* x = st + ((pu & 1) == 0 ? C::kTileBytes : 0);
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) xt[u][ks] = tile_read_t<D>(x, pu >> 1, ks, lane);
             }
         };
-        // X^T P (or dS) with P / dS read as B operands, keys 32 kb + l32.
-        // All B operands of the step are read before the first MFMA, so one
-        // LDS round trip covers them all.
+        // X^T P (or dS) with P / dS read as B operands, keys 32 kb + l32;
+        // the wave's pairs share their matrix, hence their B operands.  All B
+        // operands of the step are read before the first MFMA, so one LDS
+        // round trip covers them all.
+        const uint32_t mat = (t >> 1) * C::kPdsBytes;  // P or dS
         auto grad = [&](const f16x8 (&xt)[kPpw][4], const FA3_LDS char* pds) {
-            f16x8 bp[4][kPpw][2];
+            f16x8 bp[4][2];
+            const FA3_LDS char* m = pds + mat;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-                for (int u = 0; u < kPpw; ++u)
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-                        bp[ks][u][kb] = lds_read_b128(pds + ((kPpw * t + u) & 1) * C::kPdsBytes,
-                                                      dst_off(32 * kb + l32, 2 * ks + h));
+                for (int kb = 0; kb < 2; ++kb)
+                    bp[ks][kb] = lds_read_b128(m, dst_off(32 * kb + l32, 2 * ks + h));
             __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
@@ -641,7 +649,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                 for (int u = 0; u < kPpw; ++u)
 #pragma unroll
                     for (int kb = 0; kb < 2; ++kb)
-                        acc[u][kb] = mfma_32x32x16(xt[u][ks], bp[ks][u][kb], acc[u][kb]);
+                        acc[u][kb] = mfma_32x32x16(xt[u][ks], bp[ks][kb], acc[u][kb]);
         };
         auto prologue = [&](const FA3_LDS char* __restrict__ s0) {
             read_xt(s0, xa);
