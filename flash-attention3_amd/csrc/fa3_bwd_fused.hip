@@ -662,8 +662,11 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
             top();
             issue(ld);
             __builtin_amdgcn_sched_barrier(0);
-            grad(xcur, prd);
+            // next tile's operands first: the LDS reads run while the score
+            // waves' (higher priority) MFMAs hold the matrix unit, and this
+            // wave's MFMAs overlap their softmax instead
             read_xt(s1, xnext);
+            grad(xcur, prd);
             __builtin_amdgcn_sched_barrier(0);
         };
         auto last = [&](const f16x8 (&xcur)[kPpw][4], const FA3_LDS char* __restrict__ prd) {
@@ -900,8 +903,11 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
             top();
             issue(ld);
             __builtin_amdgcn_sched_barrier(0);
-            grad(xcur, prd);
+            // next tile's operands first: the LDS reads run while the score
+            // waves' (higher priority) MFMAs hold the matrix unit, and this
+            // wave's MFMAs overlap their softmax instead
             read_xt(s1, xnext);
+            grad(xcur, prd);
             __builtin_amdgcn_sched_barrier(0);
         };
         auto last = [&](const f16x8 (&xcur)[4], const FA3_LDS char* __restrict__ prd) {
