@@ -33,6 +33,24 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.44269504088896340736f;
 
+// delta = sum_d fp32(dO[row, d]) * fp32(O[row, d]) of one query row: lane
+// `sub` of the row's D / 8 consecutive lanes takes one 16-byte chunk, then a
+// butterfly over those lanes (same order wherever it runs, so the preprocess
+// kernel and the fused preprocess give the same bits).
+template <int D>
+__device__ __forceinline__ float row_delta(const _Float16* dout, const _Float16* out, size_t row,
+                                           int sub) {
+    const size_t base = row * D + sub * 8;
+    const f16x8 a = *(const f16x8*)(dout + base);
+    const f16x8 b = *(const f16x8*)(out + base);
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += (float)a[i] * (float)b[i];
+#pragma unroll
+    for (int off = D / 16; off > 0; off >>= 1) acc += __shfl_xor(acc, off, D / 8);
+    return acc;
+}
+
 __device__ __forceinline__ f32x16 mfma_32x32x16(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }

@@ -34,14 +34,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
     if (row >= rows) return;  // rows % kRowsPerBlock may be non-zero only at the tail
 
-    const size_t base = (size_t)row * D + sub * 8;
-    const f16x8 a = *(const f16x8*)(dout + base);
-    const f16x8 b = *(const f16x8*)(out + base);
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc += (float)a[i] * (float)b[i];
-#pragma unroll
-    for (int off = kLanesPerRow / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kLanesPerRow);
+    const float acc = row_delta<D>(dout, out, (size_t)row, sub);
 
     if (sub == 0) {
         float l2, max_log2, inv_sum;
