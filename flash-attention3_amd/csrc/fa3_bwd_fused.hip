@@ -50,6 +50,8 @@
 namespace fa3 {
 namespace {
 
+constexpr int kMaxBalM = 128;  // split plan: at most 512 jobs, so M = QT / 2 <= 128
+
 struct FusedArgs {
     const _Float16* q;
     const _Float16* k;
@@ -87,6 +89,11 @@ struct FusedArgs {
     int bal_m;
     int cnt_kv;        // offset of the split dKV jobs' counters in `counters`
     int cnt_q;         // offset of the split dQ jobs' counters
+    // head-piece lengths (tiles) of the long jobs, x in [0, bal_m): dKV job of
+    // key tile x and dQ job of query tile bal_m + x; a length that covers the
+    // whole job means that job is not split
+    uint16_t head_kv[kMaxBalM];
+    uint16_t head_q[kMaxBalM];
     int* counters;
     float* part_kv;    // [job][piece][wave][register / 4][lane][4] fp32
     float* part_q;
@@ -972,17 +979,19 @@ __device__ __forceinline__ void job_of(const FusedArgs& a, int& g, int& pos) {
 //
 // Split plan (bal_m = M = QT / 2 > 0; causal, G = 1, few jobs): the causal
 // jobs run 1 .. QT steps, so one long job would set the kernel's length.
-// Jobs longer than M (dKV key tiles kt < M, dQ query tiles qt >= M) are cut
-// into a head piece of M tiles and a remainder, and each remainder shares a
-// workgroup with a short job of the other role:
-//   p in [0, M):    dKV key tile M + p (whole), then the dQ remainder of
-//                   query tile M + p (key tiles M .. M + p);
-//   p in [M, 2M):   dQ query tile p - M (whole), then the dKV remainder of
-//                   key tile p - M (query tiles p .. QT - 1);
-//   p in [2M, 3M):  dKV head piece of key tile p - 2M (query tiles
-//                   p - 2M .. p - M - 1);
-//   p in [3M, 4M):  dQ head piece of query tile p - 2M (key tiles 0 .. M - 1).
-// Every workgroup runs M or M + 1 steps.
+// The long jobs (dKV key tiles x < M, dQ query tiles M + x) are cut into a
+// head piece of head_kv[x] / head_q[x] tiles and a remainder, and each
+// remainder shares a workgroup with a short job of the other role
+// (x = p mod M):
+//   p in [0, M):    dKV key tile M + x (whole), then the remainder of dQ
+//                   query tile M + x (key tiles head_q[x] .. M + x);
+//   p in [M, 2M):   dQ query tile x (whole), then the remainder of dKV key
+//                   tile x (query tiles x + head_kv[x] .. QT - 1);
+//   p in [2M, 3M):  head piece of dKV key tile x;
+//   p in [3M, 4M):  head piece of dQ query tile M + x.
+// The host picks the head lengths from a cost model of the steps, prologues
+// and epilogues so that the workgroups finish together (a length covering
+// the whole job leaves it unsplit).
 template <int D, bool kCausal>
 __global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
@@ -996,22 +1005,32 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
         const int M = a.bal_m;
         const int job0 = g * M;
         if (pos < M) {
-            dkv_role<D, kCausal>(a, g, M + pos, M + pos, QT, -1, smem);
-            wait_vm_lgkm0<0>();
-            barrier();
-            dq_role<D, kCausal>(a, g, M + pos, M, M + pos + 1, 2 * (job0 + pos) + 1, smem);
+            // dKV key tile M + x whole, then the remainder of dQ query tile M + x
+            const int x = pos, nq = M + x + 1, lq = a.head_q[x];
+            dkv_role<D, kCausal>(a, g, M + x, M + x, QT, -1, smem);
+            if (lq < nq) {
+                wait_vm_lgkm0<0>();
+                barrier();
+                dq_role<D, kCausal>(a, g, M + x, lq, nq, 2 * (job0 + x) + 1, smem);
+            }
         } else if (pos < 2 * M) {
-            const int x = pos - M;
+            // dQ query tile x whole, then the remainder of dKV key tile x
+            const int x = pos - M, nkv = QT - x, lkv = a.head_kv[x];
             dq_role<D, kCausal>(a, g, x, 0, x + 1, -1, smem);
-            wait_vm_lgkm0<0>();
-            barrier();
-            dkv_role<D, kCausal>(a, g, x, x + M, QT, 2 * (job0 + x) + 1, smem);
+            if (lkv < nkv) {
+                wait_vm_lgkm0<0>();
+                barrier();
+                dkv_role<D, kCausal>(a, g, x, x + lkv, QT, 2 * (job0 + x) + 1, smem);
+            }
         } else if (pos < 3 * M) {
-            const int x = pos - 2 * M;
-            dkv_role<D, kCausal>(a, g, x, x, x + M, 2 * (job0 + x), smem);
+            // head piece (or all) of dKV key tile x
+            const int x = pos - 2 * M, nkv = QT - x, lkv = a.head_kv[x];
+            dkv_role<D, kCausal>(a, g, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1,
+                                 smem);
         } else {
-            const int x = pos - 3 * M;
-            dq_role<D, kCausal>(a, g, M + x, 0, M, 2 * (job0 + x), smem);
+            // head piece (or all) of dQ query tile M + x
+            const int x = pos - 3 * M, nq = M + x + 1, lq = a.head_q[x];
+            dq_role<D, kCausal>(a, g, M + x, 0, min(lq, nq), lq < nq ? 2 * (job0 + x) : -1, smem);
         }
         return;
     }
@@ -1061,6 +1080,56 @@ void set_job_map(FusedArgs& a) {
     const bool fits = a.jobs_per_group % parts == 0;
     a.xcd_parts = fits ? parts : 0;
     a.part_len = fits ? a.jobs_per_group / parts : 0;
+}
+
+// Head-piece lengths of the split plan.  Workgroup times in units of one dKV
+// step, measured on MI355X at B1 H4 S2048 D128 (per-workgroup timestamps):
+// a dQ step costs 0.73, a unit's prologue (loads + first score phase) 2.5,
+// its epilogue 2.0 (dKV) / 0.8 (dQ) for a whole job, 2.6 / 1.6 for a head
+// piece that publishes its partial sums, 3.5 / 2.0 for the piece that adds
+// them; 0.65 at kernel entry and between two units.  For each x the pair of
+// workgroups sharing a job is balanced: the head length minimises the later
+// of the two finishing times.
+void split_heads(int M, uint16_t* head_kv, uint16_t* head_q) {
+    constexpr double kQ = 0.73, kPro = 2.5, kEntry = 0.65, kGap = 0.65;
+    constexpr double kWholeKv = 2.0, kWholeQ = 0.8, kHeadKv = 2.6, kHeadQ = 1.6;
+    constexpr double kAddKv = 3.5, kAddQ = 2.0;
+    auto unit = [&](double step, int n, double epi) { return kPro + (n - 1) * step + epi; };
+    const int QT = 2 * M;
+    for (int x = 0; x < M; ++x) {
+        // dKV key tile x (QT - x tiles): head piece alone, remainder after
+        // the whole dQ job of query tile x
+        int best = QT - x;
+        double best_t = 1e30;
+        for (int L = 1; L <= QT - x; ++L) {
+            const int r = QT - x - L;
+            const double c = kEntry + unit(1.0, L, r > 0 ? kHeadKv : kWholeKv);
+            double b = kEntry + unit(kQ, x + 1, kWholeQ);
+            if (r > 0) b += kGap + unit(1.0, r, kAddKv);
+            const double t = c > b ? c : b;
+            if (t < best_t) {
+                best_t = t;
+                best = L;
+            }
+        }
+        head_kv[x] = (uint16_t)best;
+        // dQ query tile M + x (M + x + 1 tiles): head piece alone, remainder
+        // after the whole dKV job of key tile M + x (M - x tiles)
+        best = M + x + 1;
+        best_t = 1e30;
+        for (int L = 1; L <= M + x + 1; ++L) {
+            const int r = M + x + 1 - L;
+            const double d = kEntry + unit(kQ, L, r > 0 ? kHeadQ : kWholeQ);
+            double av = kEntry + unit(1.0, M - x, kWholeKv);
+            if (r > 0) av += kGap + unit(kQ, r, kAddQ);
+            const double t = d > av ? d : av;
+            if (t < best_t) {
+                best_t = t;
+                best = L;
+            }
+        }
+        head_q[x] = (uint16_t)best;
+    }
 }
 
 FusedArgs base_args(const BwdProblem& p, const BwdTensors& t) {
@@ -1136,6 +1205,7 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     a.part_q = plan.bal_m > 0 ? reinterpret_cast<float*>(ws + plan.pq_off) : nullptr;
     a.part_kv_bytes = (uint32_t)(plan.pq_off - plan.pkv_off);
     a.part_q_bytes = (uint32_t)(plan.total - plan.pq_off);
+    if (plan.bal_m > 0) split_heads(plan.bal_m, a.head_kv, a.head_q);
     if (p.head_dim == 128) launch_d<128>(a, p.causal);
     else launch_d<64>(a, p.causal);
     err = hipGetLastError();
@@ -1157,7 +1227,7 @@ WorkspacePlan plan_workspace(const BwdProblem& p) {
     const long jobs = 2L * p.batch * p.heads_q * qt;
     if (p.causal && p.heads_q == p.heads_kv && qt >= 4 && qt % 2 == 0 &&
         jobs <= 512) {
-        w.bal_m = qt / 2;
+        w.bal_m = qt / 2;  // <= kMaxBalM since jobs <= 512
         const size_t split_jobs = (size_t)p.batch * p.heads_q * w.bal_m;  // per role
         const size_t kv_piece = (size_t)4 * (p.head_dim / 64) * 2 * 16 * 64 * sizeof(float);
         const size_t q_piece = (size_t)4 * (p.head_dim / 64) * 16 * 64 * sizeof(float);
