@@ -12,6 +12,7 @@
 // Extension over the reference: head_dim 64 is accepted besides 128.
 #include "shaobo_fa3_api.h"
 #include "shaobo_fa3_components.h"
+#include "shaobo_fa3_ext.h"
 
 #include <hip/hip_runtime.h>
 
@@ -114,10 +115,13 @@ fa3::BwdProblem problem_of(const ShaoboFa3Params* p) {
     return pr;
 }
 
-int finish(hipError_t err, const ShaoboFa3Params* p) {
+// sync_after_launch: the whole device for the null stream (reference
+// behaviour), the caller's stream otherwise.
+int finish(hipError_t err, const ShaoboFa3Params* p, hipStream_t stream = nullptr) {
     if (err != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
-    if (p->sync_after_launch && hipDeviceSynchronize() != hipSuccess) {
-        return SHAOBO_FA3_STATUS_HIP_ERROR;
+    if (p->sync_after_launch) {
+        const hipError_t e = stream == nullptr ? hipDeviceSynchronize() : hipStreamSynchronize(stream);
+        if (e != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
     }
     return SHAOBO_FA3_STATUS_SUCCESS;
 }
@@ -125,7 +129,8 @@ int finish(hipError_t err, const ShaoboFa3Params* p) {
 // Shared body of v2 and the legacy entry.
 int run_backward(const void* dout, const void* q, const void* k, const void* v, const void* out,
                  const void* aux0, const void* aux1, bool aux_is_lse, void* dq, void* dk,
-                 void* dv, void* softmax_d, const ShaoboFa3Params* params) {
+                 void* dv, void* softmax_d, const ShaoboFa3Params* params,
+                 hipStream_t stream = nullptr) {
     const int status = validate(params);
     if (status != SHAOBO_FA3_STATUS_SUCCESS) return status;
     if (dout == nullptr || q == nullptr || k == nullptr || v == nullptr || out == nullptr ||
@@ -151,12 +156,13 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
     t.dk = dk;
     t.dv = dv;
     t.delta = static_cast<float*>(softmax_d);
+    t.stream = stream;
     if (params->reserved_i32[15] == fa3::kStageEventTag) {
         for (int i = 0; i < 4; ++i) {
             t.stage_events[i] = static_cast<hipEvent_t>(params->reserved_ptr[4 + i]);
         }
     }
-    return finish(fa3::launch_backward(pr, t, params->workspace), params);
+    return finish(fa3::launch_backward(pr, t, params->workspace), params, stream);
 }
 
 size_t workspace_bytes_of(const ShaoboFa3Params* params) {
@@ -258,6 +264,14 @@ int shaobo_fa3_bwd_v2(const void* dout, const void* q, const void* k, const void
                       void* softmax_d, const ShaoboFa3Params* params) {
     return run_backward(dout, q, k, v, out, softmax_lse, nullptr, true, dq, dk, dv, softmax_d,
                         params);
+}
+
+int shaobo_fa3_bwd_v2_on_stream(const void* dout, const void* q, const void* k, const void* v,
+                                const void* out, const void* softmax_lse, void* dq, void* dk,
+                                void* dv, void* softmax_d, const ShaoboFa3Params* params,
+                                void* stream) {
+    return run_backward(dout, q, k, v, out, softmax_lse, nullptr, true, dq, dk, dv, softmax_d,
+                        params, static_cast<hipStream_t>(stream));
 }
 
 const char* shaobo_fa3_status_string(int status) {

@@ -1066,10 +1066,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_component_kernel(FusedArgs a)
 }
 
 template <int D>
-void launch_d(const FusedArgs& a, bool causal) {
+void launch_d(const FusedArgs& a, bool causal, hipStream_t stream) {
     const dim3 grid(a.n_groups * a.jobs_per_group);
-    if (causal) hipLaunchKernelGGL((bwd_fused_kernel<D, true>), grid, dim3(kThreads), 0, 0, a);
-    else hipLaunchKernelGGL((bwd_fused_kernel<D, false>), grid, dim3(kThreads), 0, 0, a);
+    if (causal) hipLaunchKernelGGL((bwd_fused_kernel<D, true>), grid, dim3(kThreads), 0, stream, a);
+    else hipLaunchKernelGGL((bwd_fused_kernel<D, false>), grid, dim3(kThreads), 0, stream, a);
 }
 
 // XCD-aware job map: n_groups groups of jobs_per_group jobs.
@@ -1164,18 +1164,18 @@ hipError_t launch_component(const BwdProblem& p, const BwdTensors& t, int role) 
     set_job_map(a);
     const dim3 grid(a.n_groups * a.jobs_per_group);
     if (p.head_dim == 128) {
-        if (role == 1) hipLaunchKernelGGL((bwd_component_kernel<128, 1>), grid, dim3(kThreads), 0, 0, a);
-        else hipLaunchKernelGGL((bwd_component_kernel<128, 2>), grid, dim3(kThreads), 0, 0, a);
+        if (role == 1) hipLaunchKernelGGL((bwd_component_kernel<128, 1>), grid, dim3(kThreads), 0, t.stream, a);
+        else hipLaunchKernelGGL((bwd_component_kernel<128, 2>), grid, dim3(kThreads), 0, t.stream, a);
     } else {
-        if (role == 1) hipLaunchKernelGGL((bwd_component_kernel<64, 1>), grid, dim3(kThreads), 0, 0, a);
-        else hipLaunchKernelGGL((bwd_component_kernel<64, 2>), grid, dim3(kThreads), 0, 0, a);
+        if (role == 1) hipLaunchKernelGGL((bwd_component_kernel<64, 1>), grid, dim3(kThreads), 0, t.stream, a);
+        else hipLaunchKernelGGL((bwd_component_kernel<64, 2>), grid, dim3(kThreads), 0, t.stream, a);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace) {
     auto mark = [&](int i) {
-        if (t.stage_events[i] != nullptr) (void)hipEventRecord(t.stage_events[i], 0);
+        if (t.stage_events[i] != nullptr) (void)hipEventRecord(t.stage_events[i], t.stream);
     };
     const WorkspacePlan plan = plan_workspace(p);
     char* ws = static_cast<char*>(workspace);
@@ -1206,8 +1206,8 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     a.part_kv_bytes = (uint32_t)(plan.pq_off - plan.pkv_off);
     a.part_q_bytes = (uint32_t)(plan.total - plan.pq_off);
     if (plan.bal_m > 0) split_heads(plan.bal_m, a.head_kv, a.head_q);
-    if (p.head_dim == 128) launch_d<128>(a, p.causal);
-    else launch_d<64>(a, p.causal);
+    if (p.head_dim == 128) launch_d<128>(a, p.causal, t.stream);
+    else launch_d<64>(a, p.causal, t.stream);
     err = hipGetLastError();
     mark(2);
     mark(3);

@@ -46,9 +46,12 @@ struct BwdTensors {
     // delta_in together with the raw max / sum pair in aux0 / aux1 (dQ).
     const float* packed_in = nullptr;
     const float* delta_in = nullptr;
-    // Optional profiling events recorded on the null stream at the stage
+    // Optional profiling events recorded on the launch stream at the stage
     // boundaries: before preprocess, before main, before dQ finalize, after.
     hipEvent_t stage_events[4] = {nullptr, nullptr, nullptr, nullptr};
+    // Stream of every launch (null: the legacy default stream, as in the
+    // reference ABI; the stream entry points pass the caller's).
+    hipStream_t stream = nullptr;
 };
 
 // params->reserved_i32[15] == kStageEventTag enables stage_events, taken

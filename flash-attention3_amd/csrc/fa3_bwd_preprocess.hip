@@ -68,12 +68,12 @@ hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, f
     if (blocks * 256 < n_counters) blocks = (n_counters + 255) / 256;
     const float scale_log2 = p.scale * kLog2e;
     if (t.aux_is_lse) {
-        hipLaunchKernelGGL((preprocess_kernel<D, true>), dim3(blocks), dim3(256), 0, 0,
+        hipLaunchKernelGGL((preprocess_kernel<D, true>), dim3(blocks), dim3(256), 0, t.stream,
                            (const _Float16*)t.dout, (const _Float16*)t.out, t.aux0, t.aux1,
                            t.delta, lse2, ndelta, t.packed, counters, n_counters, rows,
                            scale_log2);
     } else {
-        hipLaunchKernelGGL((preprocess_kernel<D, false>), dim3(blocks), dim3(256), 0, 0,
+        hipLaunchKernelGGL((preprocess_kernel<D, false>), dim3(blocks), dim3(256), 0, t.stream,
                            (const _Float16*)t.dout, (const _Float16*)t.out, t.aux0, t.aux1,
                            t.delta, lse2, ndelta, t.packed, counters, n_counters, rows,
                            scale_log2);
@@ -103,7 +103,7 @@ hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* lse2
                            int* counters, int n_counters) {
     const int rows = p.batch * p.heads_q * p.seqlen;
     const int n = rows > n_counters ? rows : n_counters;
-    hipLaunchKernelGGL(rowstats_kernel, dim3((n + 255) / 256), dim3(256), 0, 0, t.packed_in,
+    hipLaunchKernelGGL(rowstats_kernel, dim3((n + 255) / 256), dim3(256), 0, t.stream, t.packed_in,
                        lse2, ndelta, counters, n_counters, rows);
     return hipGetLastError();
 }

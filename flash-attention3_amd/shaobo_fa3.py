@@ -33,6 +33,7 @@ EXPORTS = (
     "shaobo_fa3_bwd_fused5_workspace_bytes", "shaobo_fa3_bwd_fused5",
     "shaobo_fa3_bwd_dkv_workspace_bytes", "shaobo_fa3_bwd_dkv",
     "shaobo_fa3_bwd_dq_workspace_bytes", "shaobo_fa3_bwd_dq",
+    "shaobo_fa3_bwd_v2_on_stream",
 )
 
 # Component path selectors (params.dkv_path / params.dq_path) of the canonical

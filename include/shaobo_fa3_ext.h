@@ -1,0 +1,40 @@
+/*
+ * shaobo_fa3_ext.h -- extensions of libshaobo_fa3_bwd.so beyond the
+ * reference ABI.
+ */
+#ifndef SHAOBO_FA3_EXT_H_
+#define SHAOBO_FA3_EXT_H_
+
+#include "shaobo_fa3_api.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* shaobo_fa3_bwd_v2 on a caller-chosen stream.  No counterpart in the
+ * reference, whose ABI launches on the null stream only
+ * (reference include/shaobo_fa3_api.h:119-130); this is for framework
+ * bindings that order work on their own streams (a PyTorch custom op passes
+ * torch.cuda.current_stream()).  `stream` is a hipStream_t (NULL = the null
+ * stream, which makes this identical to shaobo_fa3_bwd_v2).  Validation,
+ * statuses, workspace and outputs are those of shaobo_fa3_bwd_v2;
+ * sync_after_launch synchronises `stream` (the device for NULL).  The
+ * workspace must not be shared by calls that may run concurrently. */
+int shaobo_fa3_bwd_v2_on_stream(const void* dout,
+                                const void* q,
+                                const void* k,
+                                const void* v,
+                                const void* out,
+                                const void* softmax_lse,
+                                void* dq,
+                                void* dk,
+                                void* dv,
+                                void* softmax_d,
+                                const ShaoboFa3Params* params,
+                                void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* SHAOBO_FA3_EXT_H_ */
