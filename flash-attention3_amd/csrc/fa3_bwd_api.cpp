@@ -91,8 +91,12 @@ int validate(const ShaoboFa3Params* p) {
         p->seqused_k == nullptr && (p->max_seqlen_q == 0 || p->max_seqlen_q == p->seqlen_q) &&
         (p->max_seqlen_k == 0 || p->max_seqlen_k == p->seqlen_k) &&
         (p->total_q == 0 || p->total_q == total_q) && (p->total_k == 0 || p->total_k == total_k);
-    if (!fixed_length || p->dtype != SHAOBO_FA3_DTYPE_FP16 ||
-        p->layout != SHAOBO_FA3_LAYOUT_BHSD || !head_dim_supported(p->head_dim_qk) ||
+    // Extensions over the reference: bf16 and BSHD (its capability bits
+    // exist, its kernels reject them), head_dim 64.
+    const bool dtype_ok = p->dtype == SHAOBO_FA3_DTYPE_FP16 || p->dtype == SHAOBO_FA3_DTYPE_BF16;
+    const bool layout_ok =
+        p->layout == SHAOBO_FA3_LAYOUT_BHSD || p->layout == SHAOBO_FA3_LAYOUT_BSHD;
+    if (!fixed_length || !dtype_ok || !layout_ok || !head_dim_supported(p->head_dim_qk) ||
         p->head_dim_v != p->head_dim_qk || p->seqlen_q != p->seqlen_k ||
         p->seqlen_q % kSequenceAlignment != 0 || p->dropout_p != 0.0f || p->softcap != 0.0f ||
         p->sm_margin != 0 || !window_is_full(p)) {
@@ -110,6 +114,8 @@ fa3::BwdProblem problem_of(const ShaoboFa3Params* p) {
     pr.head_dim = p->head_dim_qk;
     pr.causal = p->causal != 0;
     pr.deterministic = p->deterministic != 0;
+    pr.bf16 = p->dtype == SHAOBO_FA3_DTYPE_BF16;
+    pr.bshd = p->layout == SHAOBO_FA3_LAYOUT_BSHD;
     pr.scale = p->softmax_scale_is_set ? p->softmax_scale
                                        : 1.0f / std::sqrt((float)p->head_dim_qk);
     return pr;
@@ -242,10 +248,10 @@ int shaobo_fa3_bwd_get_capabilities(ShaoboFa3BwdCapabilities* caps) {
     }
     caps->api_version = SHAOBO_FA3_API_VERSION;
     caps->feature_mask = SHAOBO_FA3_BWD_FEATURE_FIXED_LENGTH | SHAOBO_FA3_BWD_FEATURE_FP16 |
-                         SHAOBO_FA3_BWD_FEATURE_CAUSAL | SHAOBO_FA3_BWD_FEATURE_GQA |
-                         SHAOBO_FA3_BWD_FEATURE_DETERMINISTIC |
-                         SHAOBO_FA3_BWD_FEATURE_SOFTMAX_LSE | SHAOBO_FA3_BWD_FEATURE_BHSD |
-                         SHAOBO_FA3_BWD_FEATURE_FULL_ATTENTION;
+                         SHAOBO_FA3_BWD_FEATURE_BF16 | SHAOBO_FA3_BWD_FEATURE_CAUSAL |
+                         SHAOBO_FA3_BWD_FEATURE_GQA | SHAOBO_FA3_BWD_FEATURE_DETERMINISTIC |
+                         SHAOBO_FA3_BWD_FEATURE_SOFTMAX_LSE | SHAOBO_FA3_BWD_FEATURE_BSHD |
+                         SHAOBO_FA3_BWD_FEATURE_BHSD | SHAOBO_FA3_BWD_FEATURE_FULL_ATTENTION;
     caps->min_head_dim = kMinHeadDim;
     caps->max_head_dim = kMaxHeadDim;
     caps->head_dim_alignment = kMinHeadDim;

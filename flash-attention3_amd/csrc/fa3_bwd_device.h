@@ -22,6 +22,7 @@
 namespace fa3 {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -33,19 +34,26 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.44269504088896340736f;
 
-// delta = sum_d fp32(dO[row, d]) * fp32(O[row, d]) of one query row: lane
+// delta = sum_d fp32(dO[row, d]) * fp32(O[row, d]) of one query row whose
+// elements start at `elem` (fp16, or bf16 when kBf16): lane
 // `sub` of the row's D / 8 consecutive lanes takes one 16-byte chunk, then a
 // butterfly over those lanes (same order wherever it runs, so the preprocess
 // kernel and the fused preprocess give the same bits).
-template <int D>
-__device__ __forceinline__ float row_delta(const _Float16* dout, const _Float16* out, size_t row,
+template <int D, bool kBf16 = false>
+__device__ __forceinline__ float row_delta(const _Float16* dout, const _Float16* out, size_t elem,
                                            int sub) {
-    const size_t base = row * D + sub * 8;
+    const size_t base = elem + sub * 8;
     const f16x8 a = *(const f16x8*)(dout + base);
     const f16x8 b = *(const f16x8*)(out + base);
     float acc = 0.f;
+    if constexpr (kBf16) {
+        const bf16x8 ab = __builtin_bit_cast(bf16x8, a), bb = __builtin_bit_cast(bf16x8, b);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc += (float)a[i] * (float)b[i];
+        for (int i = 0; i < 8; ++i) acc += (float)ab[i] * (float)bb[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc += (float)a[i] * (float)b[i];
+    }
 #pragma unroll
     for (int off = D / 16; off > 0; off >>= 1) acc += __shfl_xor(acc, off, D / 8);
     return acc;

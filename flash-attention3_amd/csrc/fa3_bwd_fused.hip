@@ -67,10 +67,14 @@ struct FusedArgs {
     const float* smax;   // [B*Hq*S]
     const float* ssum;
     const float* delta;
-    void* dq;          // fp16, or fp32 when out_f32
+    void* dq;          // fp16 / bf16 (the inputs' type), or fp32 when out_f32
     void* dk;
     void* dv;
     int out_f32;
+    // element strides of one sequence row and one head in the q-side (Q, O,
+    // dO, dQ) and kv-side (K, V, dK, dV) tensors: BHSD (D, S D) or BSHD
+    // (H D, D); a batch is H S D elements in both layouts
+    int q_rs, q_hs, kv_rs, kv_hs;
     int seqlen;
     int heads_q;
     int heads_kv;
@@ -151,8 +155,29 @@ __device__ __forceinline__ void barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// 16-bit operands travel as f16x8 bits whatever their type; kBf16 selects
+// the bf16 instruction.
+template <bool kBf16>
 __device__ __forceinline__ f32x4 mfma_16x16x32(f16x8 a, f16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    if constexpr (kBf16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+template <bool kBf16>
+__device__ __forceinline__ f32x16 mfma_32x32x16t(f16x8 a, f16x8 b, f32x16 c) {
+    if constexpr (kBf16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return mfma_32x32x16(a, b, c);
+}
+// fp32 -> the 16-bit operand type (round to nearest even), as f16 bits
+template <bool kBf16>
+__device__ __forceinline__ _Float16 to16(float x) {
+    if constexpr (kBf16) return __builtin_bit_cast(_Float16, (__bf16)x);
+    else return (_Float16)x;
 }
 
 // Direct-to-LDS copy of a row-major [64][D] fp16 tile into a swizzled LDS
@@ -161,7 +186,7 @@ __device__ __forceinline__ f32x4 mfma_16x16x32(f16x8 a, f16x8 b, f32x4 c) {
 // source byte offset within the global tile is precomputed once.
 template <int D>
 __device__ __forceinline__ void tile_load_offsets(uint32_t (&off)[Cfg<D>::kLoadsPerTile],
-                                                  int wave, int lane) {
+                                                  int wave, int lane, int row_stride) {
     using C = Cfg<D>;
 #pragma unroll
     for (int j = 0; j < C::kLoadsPerTile; ++j) {
@@ -172,7 +197,7 @@ __device__ __forceinline__ void tile_load_offsets(uint32_t (&off)[Cfg<D>::kLoads
         if constexpr (C::kChunks == 16) sw = ((row & 3) << 2) | ((row >> 2) & 3);
         else sw = swz128(row);
         const int logical = (phys ^ sw) & (C::kChunks - 1);
-        off[j] = (uint32_t)((row * D + logical * 8) * 2);
+        off[j] = (uint32_t)((row * row_stride + logical * 8) * 2);
     }
 }
 
@@ -263,25 +288,33 @@ __device__ __forceinline__ uint32_t pds_off4(int r, int q) {
     return dst_off(r, q >> 1) + (q & 1) * 8;
 }
 
+// Element offset of sequence row s of head h in batch b.
+template <int D>
+__device__ __forceinline__ size_t q_elem(const FusedArgs& a, int b, int h, int s) {
+    return (size_t)b * a.heads_q * a.seqlen * D + (size_t)h * a.q_hs + (size_t)s * a.q_rs;
+}
+template <int D>
+__device__ __forceinline__ size_t kv_elem(const FusedArgs& a, int b, int h, int s) {
+    return (size_t)b * a.heads_kv * a.seqlen * D + (size_t)h * a.kv_hs + (size_t)s * a.kv_rs;
+}
+
 // ----------------------------------------------------------------------------
 // Outputs
 // ----------------------------------------------------------------------------
-// Four consecutive output elements (row-major, element offset `off`), fp16
-// or fp32.
+// Four consecutive output elements (element offset `off`): the inputs'
+// 16-bit type, or fp32.
+template <bool kBf16>
 __device__ __forceinline__ void store4(const FusedArgs& a, void* base, size_t off, f32x4 v) {
     if (a.out_f32) {
         *(f32x4*)((float*)base + off) = v;
     } else {
         f16x4 o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = (_Float16)v[e];
+        for (int e = 0; e < 4; ++e) o[e] = to16<kBf16>(v[e]);
         *(f16x4*)((_Float16*)base + off) = o;
     }
 }
 
-// dV^T / dK^T accumulators of gradient wave t (pairs kPpw t .. +kPpw, pair =
-// 2 db + matrix) to dV / dK; lane: key 32 kb + l32,
-// d = 32 db + 8 (i / 4) + 4 h + i % 4.
 // (matrix, D slice) pair u of dKV gradient wave t, as pu = 2 slice + matrix
 // (matrix 0: dV from dO and P, 1: dK from Q and dS).  Waves 0, 1 own dV and
 // waves 2, 3 own dK, each for D / 64 consecutive 32-wide slices, so a wave
@@ -291,17 +324,22 @@ __device__ __forceinline__ int dkv_pair(int t, int u) {
     return 2 * ((D / 64) * (t & 1) + u) + (t >> 1);
 }
 
-template <int D>
+// dV^T / dK^T accumulators of gradient wave t (pairs dkv_pair(t, u)) to dV /
+// dK of KV head bkv, keys kbase ..; lane: key 32 kb + l32,
+// d = 32 slice + 8 (i / 4) + 4 h + i % 4.
+template <int D, bool kBf16>
 __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase, int t, int lane,
                                           const f32x16 (&acc)[D / 64][2]) {
     constexpr int kPpw = D / 64;
     const int l32 = lane & 31, h = lane >> 5;
+    const int b = bkv / a.heads_kv;
+    const size_t base = kv_elem<D>(a, b, bkv - b * a.heads_kv, kbase);
 #pragma unroll
     for (int u = 0; u < kPpw; ++u) {
         const int pu = dkv_pair<D>(t, u);
         const float mul = (pu & 1) == 0 ? 1.f : a.scale;
         void* outp = (pu & 1) == 0 ? a.dv : a.dk;
-        const size_t off0 = ((size_t)bkv * a.seqlen + kbase) * D + 32 * (pu >> 1) + 4 * h;
+        const size_t off0 = base + 32 * (pu >> 1) + 4 * h;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -309,22 +347,22 @@ __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase
                 f32x4 v;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = acc[u][kb][4 * a4 + e] * mul;
-                store4(a, outp, off0 + (size_t)(32 * kb + l32) * D + 8 * a4, v);
+                store4<kBf16>(a, outp, off0 + (size_t)(32 * kb + l32) * a.kv_rs + 8 * a4, v);
             }
         }
     }
 }
 
-// dQ^T accumulators of gradient wave t to dQ; lane: row 32 rb + l32,
-// d = 32 db + 8 (i / 4) + 4 h + i % 4.
-template <int D>
-__device__ __forceinline__ void store_dq(const FusedArgs& a, size_t row0, int t, int lane,
+// dQ^T accumulators of gradient wave t to the dQ tile at element `base`;
+// lane: row 32 rb + l32, d = 32 db + 8 (i / 4) + 4 h + i % 4.
+template <int D, bool kBf16>
+__device__ __forceinline__ void store_dq(const FusedArgs& a, size_t base, int t, int lane,
                                          const f32x16 (&acc)[D / 64]) {
     constexpr int kRb = D / 64;
     const int db = D == 128 ? t : t >> 1;
     const int rb0 = D == 128 ? 0 : t & 1;
     const int l32 = lane & 31, h = lane >> 5;
-    const size_t off0 = row0 * D + 32 * db + 4 * h;
+    const size_t off0 = base + 32 * db + 4 * h;
 #pragma unroll
     for (int r = 0; r < kRb; ++r) {
 #pragma unroll
@@ -332,7 +370,7 @@ __device__ __forceinline__ void store_dq(const FusedArgs& a, size_t row0, int t,
             f32x4 v;
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = acc[r][4 * a4 + e] * a.scale;
-            store4(a, a.dq, off0 + (size_t)(32 * (rb0 + r) + l32) * D + 8 * a4, v);
+            store4<kBf16>(a, a.dq, off0 + (size_t)(32 * (rb0 + r) + l32) * a.q_rs + 8 * a4, v);
         }
     }
 }
@@ -427,7 +465,7 @@ __device__ __forceinline__ void split_peek(const int* counter, FA3_LDS int* flag
 // Streams query tiles [qa, qb) of every query head of the group.  slot < 0:
 // the job is whole and writes dK / dV; otherwise the unit is piece slot & 1
 // of split job slot >> 1 and the pieces' partial sums meet in split_end.
-template <int D, bool kCausal, int kRows = 0>
+template <int D, bool kCausal, bool kBf16, int kRows = 0>
 __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, int slot,
                          FA3_LDS char* smem) {
     static_assert(kRows == 0 || kRows == 1, "dKV rows come as lse2/-delta or packed");
@@ -446,22 +484,24 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
     const int kbase = kt * 64;
     const int n_it = group * (qb - qa);
 
-    uint32_t ld_off[C::kLoadsPerTile];
-    tile_load_offsets<D>(ld_off, w, lane);
+    uint32_t ld_off[C::kLoadsPerTile], kv_off[C::kLoadsPerTile];
+    tile_load_offsets<D>(ld_off, w, lane, a.q_rs);
+    tile_load_offsets<D>(kv_off, w, lane, a.kv_rs);
 
     // Cursor of the next query tile to load; a finished stream keeps
     // re-loading its last tile (into a stage nobody reads), so every step
     // issues the same loads.  All eight waves take part in every load.
-    int ld_bhq = b * a.heads_q + hkv * group, ld_qt = qa, ld_left = n_it;
+    int ld_h = hkv * group, ld_qt = qa, ld_left = n_it;
     auto issue = [&](FA3_LDS char* st) {
-        const size_t row0 = (size_t)ld_bhq * S + ld_qt * 64;
-        load_tile_async<D>(st, a.q + row0 * D, ld_off, w);
-        load_tile_async<D>(st + C::kTileBytes, a.dout + row0 * D, ld_off, w);
+        const size_t row0 = ((size_t)b * a.heads_q + ld_h) * S + ld_qt * 64;  // statistics row
+        const size_t e0 = q_elem<D>(a, b, ld_h, ld_qt * 64);
+        load_tile_async<D>(st, a.q + e0, ld_off, w);
+        load_tile_async<D>(st + C::kTileBytes, a.dout + e0, ld_off, w);
         load_rows_async<kRows>(st + 2 * C::kTileBytes, a, row0, w, lane);
         if (--ld_left > 0) {
             if (++ld_qt == qb) {
                 ld_qt = qa;
-                ++ld_bhq;
+                ++ld_h;
             }
         }
     };
@@ -484,9 +524,9 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
     FA3_LDS char* pds1 = pds0 + 2 * C::kPdsBytes;
     auto prologue_loads = [&]() {
         // this key tile's K and V are staged in the P / dS area
-        const size_t k0 = (size_t)bkv * S + kbase;
-        load_tile_async<D>(pds0, a.k + k0 * D, ld_off, w);
-        load_tile_async<D>(pds0 + C::kTileBytes, a.v + k0 * D, ld_off, w);
+        const size_t k0 = kv_elem<D>(a, b, hkv, kbase);
+        load_tile_async<D>(pds0, a.k + k0, kv_off, w);
+        load_tile_async<D>(pds0 + C::kTileBytes, a.v + k0, kv_off, w);
         issue(st_ld);
         issue(st_1);
         issue(st_2);
@@ -539,8 +579,8 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
             for (int s = 0; s < C::kKs; ++s) {
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb) {
-                    sacc[kb] = mfma_16x16x32(aq[s], kf[kb][s], s == 0 ? f32x4{} : sacc[kb]);
-                    pacc[kb] = mfma_16x16x32(ad[s], vf[kb][s], s == 0 ? ndl : pacc[kb]);
+                    sacc[kb] = mfma_16x16x32<kBf16>(aq[s], kf[kb][s], s == 0 ? f32x4{} : sacc[kb]);
+                    pacc[kb] = mfma_16x16x32<kBf16>(ad[s], vf[kb][s], s == 0 ? ndl : pacc[kb]);
                 }
             }
             set_prio<0>();
@@ -566,8 +606,8 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                 f16x4 pv, dv;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    pv[i] = (_Float16)p[4 * kb + i];
-                    dv[i] = (_Float16)ds[4 * kb + i];
+                    pv[i] = to16<kBf16>(p[4 * kb + i]);
+                    dv[i] = to16<kBf16>(ds[4 * kb + i]);
                 }
                 const uint32_t off = pds_off4(16 * kb + l16, 4 * t + g4);
                 lds_write_b64(pds, off, pv);
@@ -656,7 +696,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                 for (int u = 0; u < kPpw; ++u)
 #pragma unroll
                     for (int kb = 0; kb < 2; ++kb)
-                        acc[u][kb] = mfma_32x32x16(xt[u][ks], bp[ks][kb], acc[u][kb]);
+                        acc[u][kb] = mfma_32x32x16t<kBf16>(xt[u][ks], bp[ks][kb], acc[u][kb]);
         };
         auto prologue = [&](const FA3_LDS char* __restrict__ s0) {
             read_xt(s0, xa);
@@ -696,7 +736,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
             last(xa, pds0);
         }
         if (slot < 0) {
-            store_dkv<D>(a, bkv, kbase, t, lane, acc);
+            store_dkv<D, kBf16>(a, bkv, kbase, t, lane, acc);
             return;
         }
         // partial sums: [piece][wave][2 kPpw accumulator blocks]
@@ -707,7 +747,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         if (split_end(a.counters + a.cnt_kv + (slot >> 1), flag,
                       [&] { put_partials<kBlk>(pr, part(slot), flat, lane); })) {
             add_partials<kBlk>(pr, part(slot ^ 1), flat, lane);
-            store_dkv<D>(a, bkv, kbase, t, lane, acc);
+            store_dkv<D, kBf16>(a, bkv, kbase, t, lane, acc);
         }
     }
 }
@@ -717,7 +757,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
 // ----------------------------------------------------------------------------
 // Streams key tiles [ka, kb) (the causal diagonal, key tile qt, is masked).
 // slot: as for dkv_role.
-template <int D, bool kCausal, int kRows = 0>
+template <int D, bool kCausal, bool kBf16, int kRows = 0>
 __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int slot,
                         FA3_LDS char* smem) {
     static_assert(kRows == 0 || kRows == 2, "dQ rows come as lse2/-delta or max/sum/delta");
@@ -732,18 +772,22 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
     const int QT = S / 64;
     const int group = a.heads_q / a.heads_kv;
     const int b = bhq / a.heads_q;
-    const int bkv = b * a.heads_kv + (bhq % a.heads_q) / group;
-    const size_t row0 = (size_t)bhq * S + qt * 64;
+    const int hq = bhq - b * a.heads_q;
+    const int hkv = hq / group;
+    const size_t row0 = (size_t)bhq * S + qt * 64;  // statistics row
+    const size_t q0 = q_elem<D>(a, b, hq, qt * 64);  // this tile's Q / dO / dQ elements
     const int n_kt = kb - ka;
 
-    uint32_t ld_off[C::kLoadsPerTile];
-    tile_load_offsets<D>(ld_off, w, lane);
-    const _Float16* kh = a.k + (size_t)bkv * S * D;
-    const _Float16* vh = a.v + (size_t)bkv * S * D;
+    uint32_t ld_off[C::kLoadsPerTile], q_off[C::kLoadsPerTile];
+    tile_load_offsets<D>(ld_off, w, lane, a.kv_rs);
+    tile_load_offsets<D>(q_off, w, lane, a.q_rs);
+    const _Float16* kh = a.k + kv_elem<D>(a, b, hkv, 0);
+    const _Float16* vh = a.v + kv_elem<D>(a, b, hkv, 0);
     int ld_kt = ka;
     auto issue = [&](FA3_LDS char* st) {
-        load_tile_async<D>(st, kh + (size_t)ld_kt * 64 * D, ld_off, w);
-        load_tile_async<D>(st + C::kTileBytes, vh + (size_t)ld_kt * 64 * D, ld_off, w);
+        const size_t e = (size_t)ld_kt * 64 * a.kv_rs;
+        load_tile_async<D>(st, kh + e, ld_off, w);
+        load_tile_async<D>(st + C::kTileBytes, vh + e, ld_off, w);
         if (ld_kt + 1 < kb) ++ld_kt;
     };
     auto top = [&]() {
@@ -766,8 +810,8 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
     auto prologue_loads = [&]() {
         // this query tile's Q and dO are staged in the dS area, its lse2 and
         // -delta in the (otherwise unused) rows slot of stage 0
-        load_tile_async<D>(ds0, a.q + row0 * D, ld_off, w);
-        load_tile_async<D>(ds0 + C::kTileBytes, a.dout + row0 * D, ld_off, w);
+        load_tile_async<D>(ds0, a.q + q0, q_off, w);
+        load_tile_async<D>(ds0 + C::kTileBytes, a.dout + q0, q_off, w);
         load_rows_async<kRows>(st_ld + 2 * C::kTileBytes, a, row0, w, lane);
         issue(st_ld);
         issue(st_1);
@@ -797,8 +841,8 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
             for (int s = 0; s < C::kKs; ++s) {
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb) {
-                    sacc[rb] = mfma_16x16x32(ak[s], qf[rb][s], s == 0 ? f32x4{} : sacc[rb]);
-                    pacc[rb] = mfma_16x16x32(av[s], df[rb][s], s == 0 ? ndl[rb] : pacc[rb]);
+                    sacc[rb] = mfma_16x16x32<kBf16>(ak[s], qf[rb][s], s == 0 ? f32x4{} : sacc[rb]);
+                    pacc[rb] = mfma_16x16x32<kBf16>(av[s], df[rb][s], s == 0 ? ndl[rb] : pacc[rb]);
                 }
             }
             set_prio<0>();
@@ -818,7 +862,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
             for (int rb = 0; rb < 4; ++rb) {
                 f16x4 dv;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) dv[i] = (_Float16)p[4 * rb + i];
+                for (int i = 0; i < 4; ++i) dv[i] = to16<kBf16>(p[4 * rb + i]);
                 lds_write_b64(ds, pds_off4(16 * rb + l16, 4 * t + g4), dv);
             }
         };
@@ -897,7 +941,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-                for (int r = 0; r < kRb; ++r) acc[r] = mfma_32x32x16(xt[ks], bd[ks][r], acc[r]);
+                for (int r = 0; r < kRb; ++r) acc[r] = mfma_32x32x16t<kBf16>(xt[ks], bd[ks][r], acc[r]);
         };
         auto prologue = [&](const FA3_LDS char* __restrict__ s0) {
             read_xt(s0, xa);
@@ -937,7 +981,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
             last(xa, ds0);
         }
         if (slot < 0) {
-            store_dq<D>(a, row0, t, lane, acc);
+            store_dq<D, kBf16>(a, q0, t, lane, acc);
             return;
         }
         // partial sums: [piece][wave][kRb accumulator blocks]
@@ -946,7 +990,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         if (split_end(a.counters + a.cnt_q + (slot >> 1), flag,
                       [&] { put_partials<kRb>(pr, part(slot), acc, lane); })) {
             add_partials<kRb>(pr, part(slot ^ 1), acc, lane);
-            store_dq<D>(a, row0, t, lane, acc);
+            store_dq<D, kBf16>(a, q0, t, lane, acc);
         }
     }
 }
@@ -992,7 +1036,7 @@ __device__ __forceinline__ void job_of(const FusedArgs& a, int& g, int& pos) {
 // The host picks the head lengths from a cost model of the steps, prologues
 // and epilogues so that the workgroups finish together (a length covering
 // the whole job leaves it unsplit).
-template <int D, bool kCausal>
+template <int D, bool kCausal, bool kBf16>
 __global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
@@ -1007,41 +1051,41 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_fused_kernel(FusedArgs a) {
         if (pos < M) {
             // dKV key tile M + x whole, then the remainder of dQ query tile M + x
             const int x = pos, nq = M + x + 1, lq = a.head_q[x];
-            dkv_role<D, kCausal>(a, g, M + x, M + x, QT, -1, smem);
+            dkv_role<D, kCausal, kBf16>(a, g, M + x, M + x, QT, -1, smem);
             if (lq < nq) {
                 wait_vm_lgkm0<0>();
                 barrier();
-                dq_role<D, kCausal>(a, g, M + x, lq, nq, 2 * (job0 + x) + 1, smem);
+                dq_role<D, kCausal, kBf16>(a, g, M + x, lq, nq, 2 * (job0 + x) + 1, smem);
             }
         } else if (pos < 2 * M) {
             // dQ query tile x whole, then the remainder of dKV key tile x
             const int x = pos - M, nkv = QT - x, lkv = a.head_kv[x];
-            dq_role<D, kCausal>(a, g, x, 0, x + 1, -1, smem);
+            dq_role<D, kCausal, kBf16>(a, g, x, 0, x + 1, -1, smem);
             if (lkv < nkv) {
                 wait_vm_lgkm0<0>();
                 barrier();
-                dkv_role<D, kCausal>(a, g, x, x + lkv, QT, 2 * (job0 + x) + 1, smem);
+                dkv_role<D, kCausal, kBf16>(a, g, x, x + lkv, QT, 2 * (job0 + x) + 1, smem);
             }
         } else if (pos < 3 * M) {
             // head piece (or all) of dKV key tile x
             const int x = pos - 2 * M, nkv = QT - x, lkv = a.head_kv[x];
-            dkv_role<D, kCausal>(a, g, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1,
+            dkv_role<D, kCausal, kBf16>(a, g, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1,
                                  smem);
         } else {
             // head piece (or all) of dQ query tile M + x
             const int x = pos - 3 * M, nq = M + x + 1, lq = a.head_q[x];
-            dq_role<D, kCausal>(a, g, M + x, 0, min(lq, nq), lq < nq ? 2 * (job0 + x) : -1, smem);
+            dq_role<D, kCausal, kBf16>(a, g, M + x, 0, min(lq, nq), lq < nq ? 2 * (job0 + x) : -1, smem);
         }
         return;
     }
     const int level = pos / (group + 1);
     const int slot = pos % (group + 1);
     if (slot == 0) {
-        dkv_role<D, kCausal>(a, g, level, kCausal ? level : 0, QT, -1, smem);
+        dkv_role<D, kCausal, kBf16>(a, g, level, kCausal ? level : 0, QT, -1, smem);
     } else {
         const int b = g / a.heads_kv, hkv = g % a.heads_kv;
         const int qt = QT - 1 - level;
-        dq_role<D, kCausal>(a, b * a.heads_q + hkv * group + slot - 1, qt, 0, kCausal ? qt + 1 : QT,
+        dq_role<D, kCausal, kBf16>(a, b * a.heads_q + hkv * group + slot - 1, qt, 0, kCausal ? qt + 1 : QT,
                             -1, smem);
     }
 }
@@ -1058,18 +1102,23 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_component_kernel(FusedArgs a)
     job_of(a, g, pos);
     const int QT = a.seqlen / 64;
     if constexpr (kRole == 1) {
-        dkv_role<D, true, 1>(a, g, pos, pos, QT, -1, smem);
+        dkv_role<D, true, false, 1>(a, g, pos, pos, QT, -1, smem);
     } else {
         const int qt = QT - 1 - pos;
-        dq_role<D, true, 2>(a, g, qt, 0, qt + 1, -1, smem);
+        dq_role<D, true, false, 2>(a, g, qt, 0, qt + 1, -1, smem);
     }
 }
 
 template <int D>
-void launch_d(const FusedArgs& a, bool causal, hipStream_t stream) {
+void launch_d(const FusedArgs& a, bool causal, bool bf16, hipStream_t stream) {
     const dim3 grid(a.n_groups * a.jobs_per_group);
-    if (causal) hipLaunchKernelGGL((bwd_fused_kernel<D, true>), grid, dim3(kThreads), 0, stream, a);
-    else hipLaunchKernelGGL((bwd_fused_kernel<D, false>), grid, dim3(kThreads), 0, stream, a);
+    if (bf16) {
+        if (causal) hipLaunchKernelGGL((bwd_fused_kernel<D, true, true>), grid, dim3(kThreads), 0, stream, a);
+        else hipLaunchKernelGGL((bwd_fused_kernel<D, false, true>), grid, dim3(kThreads), 0, stream, a);
+    } else {
+        if (causal) hipLaunchKernelGGL((bwd_fused_kernel<D, true, false>), grid, dim3(kThreads), 0, stream, a);
+        else hipLaunchKernelGGL((bwd_fused_kernel<D, false, false>), grid, dim3(kThreads), 0, stream, a);
+    }
 }
 
 // XCD-aware job map: n_groups groups of jobs_per_group jobs.
@@ -1142,6 +1191,10 @@ FusedArgs base_args(const BwdProblem& p, const BwdTensors& t) {
     a.dk = t.dk;
     a.dv = t.dv;
     a.out_f32 = p.out_f32 ? 1 : 0;
+    a.q_rs = p.bshd ? p.heads_q * p.head_dim : p.head_dim;
+    a.q_hs = p.bshd ? p.head_dim : p.seqlen * p.head_dim;
+    a.kv_rs = p.bshd ? p.heads_kv * p.head_dim : p.head_dim;
+    a.kv_hs = p.bshd ? p.head_dim : p.seqlen * p.head_dim;
     a.seqlen = p.seqlen;
     a.heads_q = p.heads_q;
     a.heads_kv = p.heads_kv;
@@ -1206,8 +1259,8 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     a.part_kv_bytes = (uint32_t)(plan.pq_off - plan.pkv_off);
     a.part_q_bytes = (uint32_t)(plan.total - plan.pq_off);
     if (plan.bal_m > 0) split_heads(plan.bal_m, a.head_kv, a.head_q);
-    if (p.head_dim == 128) launch_d<128>(a, p.causal, t.stream);
-    else launch_d<64>(a, p.causal, t.stream);
+    if (p.head_dim == 128) launch_d<128>(a, p.causal, p.bf16, t.stream);
+    else launch_d<64>(a, p.causal, p.bf16, t.stream);
     err = hipGetLastError();
     mark(2);
     mark(3);

@@ -25,6 +25,8 @@ struct BwdProblem {
     bool deterministic = false;
     float scale = 0.f;  // softmax scale
     bool out_f32 = false;  // outputs fp32 (component entries) instead of fp16
+    bool bf16 = false;     // 16-bit tensors are bf16 (fp16 otherwise)
+    bool bshd = false;     // tensors are [B, S, H, D] (BHSD otherwise); rows stay [B, Hq, S]
 };
 
 struct BwdTensors {

@@ -19,13 +19,15 @@
 namespace fa3 {
 namespace {
 
-template <int D, bool kLse>
+// Rows are [B, Hq, S]; O / dO element strides of one sequence row (q_rs) and
+// one head (q_hs) cover BHSD and BSHD; kBf16: O / dO are bf16.
+template <int D, bool kLse, bool kBf16>
 __global__ __launch_bounds__(256) void preprocess_kernel(
     const _Float16* __restrict__ dout, const _Float16* __restrict__ out,
     const float* __restrict__ aux0, const float* __restrict__ aux1,
     float* __restrict__ delta, float* __restrict__ lse2, float* __restrict__ ndelta,
     float* __restrict__ packed, int* __restrict__ counters, int n_counters, int rows,
-    float scale_log2) {
+    float scale_log2, int heads_q, int seqlen, int q_rs, int q_hs) {
     constexpr int kLanesPerRow = D / 8;
     constexpr int kRowsPerBlock = 256 / kLanesPerRow;
     const int gid = blockIdx.x * 256 + threadIdx.x;
@@ -34,7 +36,10 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
     if (row >= rows) return;  // rows % kRowsPerBlock may be non-zero only at the tail
 
-    const float acc = row_delta<D>(dout, out, (size_t)row, sub);
+    const int hs = heads_q * seqlen;
+    const int b = row / hs, rem = row - b * hs, h = rem / seqlen, sq = rem - h * seqlen;
+    const size_t elem = (size_t)b * hs * D + (size_t)h * q_hs + (size_t)sq * q_rs;
+    const float acc = row_delta<D, kBf16>(dout, out, elem, sub);
 
     if (sub == 0) {
         float l2, max_log2, inv_sum;
@@ -67,16 +72,20 @@ hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, f
     int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
     if (blocks * 256 < n_counters) blocks = (n_counters + 255) / 256;
     const float scale_log2 = p.scale * kLog2e;
+    const int q_rs = p.bshd ? p.heads_q * D : D;
+    const int q_hs = p.bshd ? D : p.seqlen * D;
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), 0, t.stream, (const _Float16*)t.dout,
+                           (const _Float16*)t.out, t.aux0, t.aux1, t.delta, lse2, ndelta,
+                           t.packed, counters, n_counters, rows, scale_log2, p.heads_q, p.seqlen,
+                           q_rs, q_hs);
+    };
     if (t.aux_is_lse) {
-        hipLaunchKernelGGL((preprocess_kernel<D, true>), dim3(blocks), dim3(256), 0, t.stream,
-                           (const _Float16*)t.dout, (const _Float16*)t.out, t.aux0, t.aux1,
-                           t.delta, lse2, ndelta, t.packed, counters, n_counters, rows,
-                           scale_log2);
+        if (p.bf16) go(preprocess_kernel<D, true, true>);
+        else go(preprocess_kernel<D, true, false>);
     } else {
-        hipLaunchKernelGGL((preprocess_kernel<D, false>), dim3(blocks), dim3(256), 0, t.stream,
-                           (const _Float16*)t.dout, (const _Float16*)t.out, t.aux0, t.aux1,
-                           t.delta, lse2, ndelta, t.packed, counters, n_counters, rows,
-                           scale_log2);
+        if (p.bf16) go(preprocess_kernel<D, false, true>);
+        else go(preprocess_kernel<D, false, false>);
     }
     return hipGetLastError();
 }

@@ -21,7 +21,10 @@
 //   lse_i   = max_i * scale + ln(sum_i)                 full_bwd_correctness.cpp:229-233
 // Inputs (the build's own): Q, K, V, dO ~ N(0,1) from a
 // seeded splitmix64 + Box-Muller stream, rounded to fp16; and the reference's
-// deterministic pattern, generate_full_bwd_golden.py:135-151.
+// deterministic pattern, generate_full_bwd_golden.py:135-151.  The *_fmt
+// entry points also take bf16 tensors (the build's bf16 extension; the
+// golden defines fp16 only): the same formulas with bf16 <-> fp32 conversion
+// of the inputs and of O.
 //
 // Work is split over (head, 64-row block) with std::thread.  dQ/delta come
 // from a per-query-row pass, dK/dV from a per-key-block pass that recomputes
@@ -91,6 +94,27 @@ uint16_t f2h(float f) {
     return (uint16_t)(sign | half);
 }
 
+// ---- bf16 <-> fp32: the top 16 bits of binary32; rounding to nearest
+// even by adding 0x7fff plus the lowest kept bit before truncation; NaN
+// stays NaN (quiet bit set).
+inline float bf2f(uint16_t b) {
+    const uint32_t bits = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+inline uint16_t f2bf(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+    x += 0x7fffu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+
+// 16-bit storage format of the tensors: 0 fp16, 1 bf16.
+inline float u16_to_f32(uint16_t v, int fmt) { return fmt ? bf2f(v) : h2f(v); }
+inline uint16_t f32_to_u16(float f, int fmt) { return fmt ? f2bf(f) : f2h(f); }
+
 void to_f32(const uint16_t* src, float* dst, size_t n) {
     size_t i = 0;
 #if defined(__F16C__)
@@ -100,6 +124,14 @@ void to_f32(const uint16_t* src, float* dst, size_t n) {
     }
 #endif
     for (; i < n; ++i) dst[i] = h2f(src[i]);
+}
+
+void to_f32_fmt(const uint16_t* src, float* dst, size_t n, int fmt) {
+    if (!fmt) {
+        to_f32(src, dst, n);
+        return;
+    }
+    for (size_t i = 0; i < n; ++i) dst[i] = bf2f(src[i]);
 }
 
 inline float dot(const float* a, const float* b, int n) {
@@ -169,7 +201,7 @@ extern "C" {
 
 // N(0,1) samples rounded to fp16: splitmix64 -> two 53-bit uniforms ->
 // Box-Muller (both outputs used).  Deterministic for a given seed.
-void fa3o_randn_f16(uint16_t* out, size_t n, uint64_t seed) {
+void fa3o_randn_fmt(uint16_t* out, size_t n, uint64_t seed, int fmt) {
     uint64_t state = seed;
     auto next = [&state]() {
         uint64_t z = (state += 0x9e3779b97f4a7c15ull);
@@ -182,18 +214,27 @@ void fa3o_randn_f16(uint16_t* out, size_t n, uint64_t seed) {
         const double u1 = ((next() >> 11) + 1.0) * (1.0 / 9007199254740993.0);  // (0, 1]
         const double u2 = (next() >> 11) * (1.0 / 9007199254740992.0);          // [0, 1)
         const double rad = std::sqrt(-2.0 * std::log(u1));
-        out[i] = f2h((float)(rad * std::cos(two_pi * u2)));
-        if (i + 1 < n) out[i + 1] = f2h((float)(rad * std::sin(two_pi * u2)));
+        out[i] = f32_to_u16((float)(rad * std::cos(two_pi * u2)), fmt);
+        if (i + 1 < n) out[i + 1] = f32_to_u16((float)(rad * std::sin(two_pi * u2)), fmt);
     }
 }
+void fa3o_randn_f16(uint16_t* out, size_t n, uint64_t seed) { fa3o_randn_fmt(out, n, seed, 0); }
 
 // Reference deterministic input pattern
 // (generate_full_bwd_golden.py:135-140): fp16(fp32((idx*mul + 7) % mod - mod/2) * scale).
-void fa3o_pattern_f16(uint16_t* out, size_t n, int64_t mul, int64_t mod, float value_scale) {
+void fa3o_pattern_fmt(uint16_t* out, size_t n, int64_t mul, int64_t mod, float value_scale,
+                      int fmt) {
     for (size_t i = 0; i < n; ++i) {
         const int64_t v = (((int64_t)i * mul + 7) % mod) - (mod / 2);
-        out[i] = f2h((float)v * value_scale);
+        out[i] = f32_to_u16((float)v * value_scale, fmt);
     }
+}
+void fa3o_pattern_f16(uint16_t* out, size_t n, int64_t mul, int64_t mod, float value_scale) {
+    fa3o_pattern_fmt(out, n, mul, mod, value_scale, 0);
+}
+void fa3o_bf16_to_f32(const uint16_t* src, float* dst, size_t n) { to_f32_fmt(src, dst, n, 1); }
+void fa3o_f32_to_bf16(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = f2bf(src[i]);
 }
 
 void fa3o_f16_to_f32(const uint16_t* src, float* dst, size_t n) { to_f32(src, dst, n); }
@@ -203,9 +244,10 @@ void fa3o_f32_to_f16(const float* src, uint16_t* dst, size_t n) {
 
 // Forward: out (fp16 bits), scores_max, scores_sum, lse (natural log).
 // Only the query heads of kv groups [bkv_begin, bkv_end) are computed.
-void fa3o_forward(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16, int B, int Hq,
-                  int Hkv, int S, int D, int causal, float scale, int bkv_begin, int bkv_end,
-                  uint16_t* out16, float* smax, float* ssum, float* lse, int threads) {
+void fa3o_forward_fmt(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16, int B,
+                      int Hq, int Hkv, int S, int D, int causal, float scale, int bkv_begin,
+                      int bkv_end, uint16_t* out16, float* smax, float* ssum, float* lse,
+                      int threads, int fmt) {
     const Shape s{B, Hq, Hkv, S, D, causal, scale, bkv_begin, bkv_end};
     const int G = Hq / Hkv;
     const float scale_log2 = (float)(scale * (float)1.4426950408889634);
@@ -217,9 +259,9 @@ void fa3o_forward(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16,
         const int bkv = bkv_begin + hl / G;
         const int bh = (bkv / Hkv) * Hq + (bkv % Hkv) * G + hl % G;
         std::vector<float> qh(hsz), kh(hsz), vh(hsz), score(S), pnum(S), o(D);
-        to_f32(q16 + (size_t)bh * hsz, qh.data(), hsz);
-        to_f32(k16 + (size_t)bkv * hsz, kh.data(), hsz);
-        to_f32(v16 + (size_t)bkv * hsz, vh.data(), hsz);
+        to_f32_fmt(q16 + (size_t)bh * hsz, qh.data(), hsz, fmt);
+        to_f32_fmt(k16 + (size_t)bkv * hsz, kh.data(), hsz, fmt);
+        to_f32_fmt(v16 + (size_t)bkv * hsz, vh.data(), hsz, fmt);
         const int i1 = (rb + 1) * kRowBlock < S ? (rb + 1) * kRowBlock : S;
         for (int i = rb * kRowBlock; i < i1; ++i) {
             float mx, sm;
@@ -229,7 +271,7 @@ void fa3o_forward(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16,
             std::fill(o.begin(), o.end(), 0.f);
             for (int j = 0; j < nk; ++j) axpy(pnum[j] / sm, vh.data() + (size_t)j * D, o.data(), D);
             const size_t row = (size_t)bh * S + i;
-            for (int d = 0; d < D; ++d) out16[row * D + d] = f2h(o[d]);
+            for (int d = 0; d < D; ++d) out16[row * D + d] = f32_to_u16(o[d], fmt);
             smax[row] = mx;
             ssum[row] = sm;
             lse[row] = mx * scale + std::log(sm);
@@ -239,11 +281,11 @@ void fa3o_forward(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16,
 
 // Backward: delta, dq (fp32 [B,Hq,S,D]), dk, dv (fp32 [B,Hkv,S,D]) for the
 // kv groups [bkv_begin, bkv_end).  smax/ssum are the forward row statistics.
-void fa3o_backward(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16,
-                   const uint16_t* out16, const uint16_t* dout16, const float* smax,
-                   const float* ssum, int B, int Hq, int Hkv, int S, int D, int causal,
-                   float scale, int bkv_begin, int bkv_end, float* delta, float* dq, float* dk,
-                   float* dv, int threads) {
+void fa3o_backward_fmt(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16,
+                       const uint16_t* out16, const uint16_t* dout16, const float* smax,
+                       const float* ssum, int B, int Hq, int Hkv, int S, int D, int causal,
+                       float scale, int bkv_begin, int bkv_end, float* delta, float* dq,
+                       float* dk, float* dv, int threads, int fmt) {
     const Shape s{B, Hq, Hkv, S, D, causal, scale, bkv_begin, bkv_end};
     const int G = Hq / Hkv;
     const float scale_log2 = (float)(scale * (float)1.4426950408889634);
@@ -256,14 +298,14 @@ void fa3o_backward(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16
         O((size_t)ngroups * G * hsz), K((size_t)ngroups * hsz), V((size_t)ngroups * hsz);
     parallel_for(ngroups, threads, [&](int gl) {
         const int bkv = bkv_begin + gl;
-        to_f32(k16 + (size_t)bkv * hsz, K.data() + (size_t)gl * hsz, hsz);
-        to_f32(v16 + (size_t)bkv * hsz, V.data() + (size_t)gl * hsz, hsz);
+        to_f32_fmt(k16 + (size_t)bkv * hsz, K.data() + (size_t)gl * hsz, hsz, fmt);
+        to_f32_fmt(v16 + (size_t)bkv * hsz, V.data() + (size_t)gl * hsz, hsz, fmt);
         for (int gi = 0; gi < G; ++gi) {
             const int bh = (bkv / Hkv) * Hq + (bkv % Hkv) * G + gi;
             const size_t dst = ((size_t)gl * G + gi) * hsz;
-            to_f32(q16 + (size_t)bh * hsz, Q.data() + dst, hsz);
-            to_f32(dout16 + (size_t)bh * hsz, DO.data() + dst, hsz);
-            to_f32(out16 + (size_t)bh * hsz, O.data() + dst, hsz);
+            to_f32_fmt(q16 + (size_t)bh * hsz, Q.data() + dst, hsz, fmt);
+            to_f32_fmt(dout16 + (size_t)bh * hsz, DO.data() + dst, hsz, fmt);
+            to_f32_fmt(out16 + (size_t)bh * hsz, O.data() + dst, hsz, fmt);
         }
     });
     auto bh_of = [&](int gl, int gi) {
@@ -337,6 +379,22 @@ void fa3o_backward(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16
         std::memcpy(dk + ((size_t)bkv * S + j0) * D, dka.data(), dka.size() * sizeof(float));
         std::memcpy(dv + ((size_t)bkv * S + j0) * D, dva.data(), dva.size() * sizeof(float));
     });
+}
+
+// fp16 entry points (format 0)
+void fa3o_forward(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16, int B, int Hq,
+                  int Hkv, int S, int D, int causal, float scale, int bkv_begin, int bkv_end,
+                  uint16_t* out16, float* smax, float* ssum, float* lse, int threads) {
+    fa3o_forward_fmt(q16, k16, v16, B, Hq, Hkv, S, D, causal, scale, bkv_begin, bkv_end, out16,
+                     smax, ssum, lse, threads, 0);
+}
+void fa3o_backward(const uint16_t* q16, const uint16_t* k16, const uint16_t* v16,
+                   const uint16_t* out16, const uint16_t* dout16, const float* smax,
+                   const float* ssum, int B, int Hq, int Hkv, int S, int D, int causal,
+                   float scale, int bkv_begin, int bkv_end, float* delta, float* dq, float* dk,
+                   float* dv, int threads) {
+    fa3o_backward_fmt(q16, k16, v16, out16, dout16, smax, ssum, B, Hq, Hkv, S, D, causal, scale,
+                      bkv_begin, bkv_end, delta, dq, dk, dv, threads, 0);
 }
 
 }  // extern "C"

@@ -45,6 +45,13 @@ def lib():
                                    u16p, f32p, f32p, f32p, i]
         L.fa3o_backward.argtypes = [u16p, u16p, u16p, u16p, u16p, f32p, f32p, i, i, i, i, i, i,
                                     ctypes.c_float, i, i, f32p, f32p, f32p, f32p, i]
+        L.fa3o_forward_fmt.argtypes = L.fa3o_forward.argtypes + [i]
+        L.fa3o_backward_fmt.argtypes = L.fa3o_backward.argtypes + [i]
+        L.fa3o_randn_fmt.argtypes = [u16p, ctypes.c_size_t, ctypes.c_uint64, i]
+        L.fa3o_pattern_fmt.argtypes = [u16p, ctypes.c_size_t, ctypes.c_int64, ctypes.c_int64,
+                                       ctypes.c_float, i]
+        L.fa3o_bf16_to_f32.argtypes = [u16p, f32p, ctypes.c_size_t]
+        L.fa3o_f32_to_bf16.argtypes = [f32p, u16p, ctypes.c_size_t]
         _lib = L
     return _lib
 
@@ -69,14 +76,40 @@ def pattern_f16(shape, mul, mod, scale):
     return out.view(np.float16).reshape(shape)
 
 
-def make_inputs(B, Hq, Hkv, S, D, kind="randn", seed_offset=0):
-    """Q, K, V, dO as fp16 numpy arrays (BHSD)."""
+# bf16 tensors travel as numpy uint16 arrays of their bit patterns (numpy has
+# no bfloat16); fp16 tensors as float16.
+def randn_bf16(shape, seed):
+    out = np.empty(int(np.prod(shape)), dtype=np.uint16)
+    lib().fa3o_randn_fmt(out, out.size, seed, 1)
+    return out.reshape(shape)
+
+
+def pattern_bf16(shape, mul, mod, scale):
+    out = np.empty(int(np.prod(shape)), dtype=np.uint16)
+    lib().fa3o_pattern_fmt(out, out.size, mul, mod, scale, 1)
+    return out.reshape(shape)
+
+
+def bf16_to_f32(bits):
+    return (np.ascontiguousarray(bits).astype(np.uint32) << 16).view(np.float32)
+
+
+def to_f32(a):
+    """fp32 values of an fp16 array or of bf16 bits (uint16)."""
+    return bf16_to_f32(a) if a.dtype == np.uint16 else a.astype(np.float32)
+
+
+def make_inputs(B, Hq, Hkv, S, D, kind="randn", seed_offset=0, dtype="fp16"):
+    """Q, K, V, dO (BHSD): fp16 arrays, or bf16 bits as uint16 when dtype='bf16'."""
     qs, ks = (B, Hq, S, D), (B, Hkv, S, D)
     shapes = {"q": qs, "k": ks, "v": ks, "dout": qs}
+    bf = dtype == "bf16"
     if kind == "randn":
-        return {n: randn_f16(shapes[n], SEEDS[n] + seed_offset) for n in shapes}
+        gen = randn_bf16 if bf else randn_f16
+        return {n: gen(shapes[n], SEEDS[n] + seed_offset) for n in shapes}
     if kind == "pattern":
-        return {n: pattern_f16(shapes[n], *PATTERN[n]) for n in shapes}
+        gen = pattern_bf16 if bf else pattern_f16
+        return {n: gen(shapes[n], *PATTERN[n]) for n in shapes}
     raise ValueError(kind)
 
 
@@ -85,17 +118,19 @@ def _u16(a):
 
 
 def forward(q, k, v, causal, scale, bkv=None, threads=None):
-    """fp32 CPU forward: returns O (fp16), scores_max, scores_sum, lse (natural)."""
+    """fp32 CPU forward: returns O (the inputs' 16-bit type), scores_max,
+    scores_sum, lse (natural)."""
     B, Hq, S, D = q.shape
     Hkv = k.shape[1]
     b0, b1 = (0, B * Hkv) if bkv is None else bkv
+    fmt = 1 if q.dtype == np.uint16 else 0
     out = np.zeros((B, Hq, S, D), dtype=np.uint16)
     smax = np.zeros((B, Hq, S), np.float32)
     ssum = np.zeros((B, Hq, S), np.float32)
     lse = np.zeros((B, Hq, S), np.float32)
-    lib().fa3o_forward(_u16(q), _u16(k), _u16(v), B, Hq, Hkv, S, D, int(causal), scale, b0, b1,
-                       out, smax, ssum, lse, threads or default_threads())
-    return out.view(np.float16), smax, ssum, lse
+    lib().fa3o_forward_fmt(_u16(q), _u16(k), _u16(v), B, Hq, Hkv, S, D, int(causal), scale, b0,
+                           b1, out, smax, ssum, lse, threads or default_threads(), fmt)
+    return (out if fmt else out.view(np.float16)), smax, ssum, lse
 
 
 def backward(q, k, v, out, dout, smax, ssum, causal, scale, bkv=None, threads=None):
@@ -107,22 +142,23 @@ def backward(q, k, v, out, dout, smax, ssum, causal, scale, bkv=None, threads=No
     dq = np.zeros((B, Hq, S, D), np.float32)
     dk = np.zeros((B, Hkv, S, D), np.float32)
     dv = np.zeros((B, Hkv, S, D), np.float32)
-    lib().fa3o_backward(_u16(q), _u16(k), _u16(v), _u16(out), _u16(dout), smax, ssum, B, Hq,
-                        Hkv, S, D, int(causal), scale, b0, b1, delta, dq, dk, dv,
-                        threads or default_threads())
+    fmt = 1 if q.dtype == np.uint16 else 0
+    lib().fa3o_backward_fmt(_u16(q), _u16(k), _u16(v), _u16(out), _u16(dout), smax, ssum, B, Hq,
+                            Hkv, S, D, int(causal), scale, b0, b1, delta, dq, dk, dv,
+                            threads or default_threads(), fmt)
     return delta, dq, dk, dv
 
 
 def golden(B, Hq, Hkv, S, D, causal, scale=None, kind="randn", bkv=None, threads=None,
-           seed_offset=0):
+           seed_offset=0, dtype="fp16"):
     """Inputs + forward + backward in one call (dict of numpy arrays)."""
     scale = 1.0 / math.sqrt(D) if scale is None else scale
-    x = make_inputs(B, Hq, Hkv, S, D, kind, seed_offset)
+    x = make_inputs(B, Hq, Hkv, S, D, kind, seed_offset, dtype)
     out, smax, ssum, lse = forward(x["q"], x["k"], x["v"], causal, scale, bkv, threads)
     delta, dq, dk, dv = backward(x["q"], x["k"], x["v"], out, x["dout"], smax, ssum, causal,
                                  scale, bkv, threads)
     x.update(out=out, scores_max=smax, scores_sum=ssum, lse=lse, delta=delta, dq=dq, dk=dk,
-             dv=dv, scale=scale, causal=causal)
+             dv=dv, scale=scale, causal=causal, dtype=dtype)
     return x
 
 

@@ -88,12 +88,13 @@ def test_capabilities(lib):
     caps.struct_size = ctypes.sizeof(caps)
     assert lib.shaobo_fa3_bwd_get_capabilities(ctypes.byref(caps)) == F.SUCCESS
     required = 0
+    # the reference's bits, plus this build's BF16 and BSHD extensions
     for n in ("FIXED_LENGTH", "FP16", "CAUSAL", "GQA", "DETERMINISTIC", "SOFTMAX_LSE", "BHSD",
-              "FULL_ATTENTION"):
+              "FULL_ATTENTION", "BF16", "BSHD"):
         required |= F.FEATURES[n]
     assert caps.api_version == F.API_VERSION
     assert caps.feature_mask & required == required
-    for n in ("VARLEN", "BF16", "LOCAL_WINDOW", "SOFTCAP", "BSHD"):
+    for n in ("VARLEN", "LOCAL_WINDOW", "SOFTCAP"):
         assert not caps.feature_mask & F.FEATURES[n]
     assert caps.max_head_dim == 128 and caps.sequence_alignment == 128
     assert caps.min_head_dim == 64 and caps.head_dim_alignment == 64
@@ -108,8 +109,11 @@ CONTRACT_CASES = [
     ("local_window", {"window_left": 128}, F.UNSUPPORTED),
     ("softcap", {"softcap": 1.0}, F.UNSUPPORTED),
     ("dropout", {"dropout_p": 0.1}, F.UNSUPPORTED),
-    ("bf16", {"dtype": F.DTYPE_BF16}, F.UNSUPPORTED),
-    ("bshd", {"layout": F.LAYOUT_BSHD}, F.UNSUPPORTED),
+    # the reference rejects these two (UNSUPPORTED); this build supports them
+    ("bf16", {"dtype": F.DTYPE_BF16}, F.SUCCESS),
+    ("bshd", {"layout": F.LAYOUT_BSHD}, F.SUCCESS),
+    ("fp8", {"dtype": F.DTYPE_FP8}, F.UNSUPPORTED),
+    ("layout_3", {"layout": 3}, F.UNSUPPORTED),
     ("varlen", {"cu_seqlens_q": "ptr"}, F.UNSUPPORTED),
     ("sm_margin", {"sm_margin": 1}, F.UNSUPPORTED),
     ("negative_scale", {"softmax_scale": -1.0}, F.INVALID_VALUE),
@@ -207,7 +211,7 @@ def test_launch_error_paths_without_gpu(lib):
     p.batch = 0
     assert lib.shaobo_fa3_bwd_v2(*args, ctypes.byref(p)) == F.INVALID_VALUE
     p = supported(lib)
-    p.dtype = F.DTYPE_BF16
+    p.dtype = F.DTYPE_FP8
     assert lib.shaobo_fa3_bwd_v2(*args, ctypes.byref(p)) == F.UNSUPPORTED
     p = supported(lib)
     bad = list(args)
@@ -284,10 +288,11 @@ def test_validation_matches_reference_code(lib):
         theirs = ref.shaobo_fa3_bwd_v2_validate(ctypes.byref(p))
         seen.add(theirs)
         if mine != theirs:
-            # head_dim 64 is this build's extension: the reference rejects it
-            # as UNSUPPORTED when everything else is valid.
-            assert (p.head_dim_qk == 64 and p.head_dim_v == 64 and mine == F.SUCCESS
-                    and theirs == F.UNSUPPORTED), (mine, theirs)
+            # head_dim 64, bf16 and BSHD are this build's extensions: the
+            # reference rejects them as UNSUPPORTED when all else is valid.
+            ext = (p.head_dim_qk == 64 and p.head_dim_v == 64) or p.dtype == F.DTYPE_BF16 \
+                or p.layout == F.LAYOUT_BSHD
+            assert ext and mine == F.SUCCESS and theirs == F.UNSUPPORTED, (mine, theirs)
     assert seen == {F.SUCCESS, F.INVALID_VALUE, F.UNSUPPORTED}
     # params_init agrees byte for byte
     a, b = F.Params(), F.Params()

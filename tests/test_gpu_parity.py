@@ -226,3 +226,39 @@ def test_full_size_configs(B, Hq, Hkv, S, D, causal, bkv):
     sum_do = g["dout"].astype(np.float64).sum(axis=2).reshape(B, Hkv, G, D).sum(axis=2)
     err = np.abs(sum_dv - sum_do).max() / np.abs(sum_do).max()
     assert err < 1e-2, err
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,causal", [
+    (1, 1, 1, 128, 128, True),
+    (1, 4, 4, 2048, 128, True),   # P3 shape, split plan
+    (1, 4, 2, 256, 128, True),    # GQA
+    (2, 8, 2, 256, 128, False),
+    (1, 2, 2, 512, 64, True),
+])
+def test_v2_bf16(B, Hq, Hkv, S, D, causal):
+    """bf16 tensors (this build's extension): bf16 oracle, bf16 bar."""
+    log(f"[case] bf16 B={B} Hq={Hq} Hkv={Hkv} S={S} D={D} causal={causal}")
+    g = O.golden(B, Hq, Hkv, S, D, causal, dtype="bf16")
+    res = run_v2(g, torch)
+    assert res["status"] == F.SUCCESS, F.status_name(res["status"])
+    rep = check(res, g)
+    log({k: round(v["max_rel"], 6) for k, v in rep.items()})
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,causal,dtype", [
+    (1, 4, 4, 2048, 128, True, "fp16"),   # split plan
+    (2, 8, 2, 256, 128, False, "fp16"),   # GQA, batch 2
+    (1, 4, 2, 384, 64, True, "fp16"),
+    (2, 4, 2, 256, 128, True, "bf16"),
+])
+def test_v2_bshd(B, Hq, Hkv, S, D, causal, dtype):
+    """[B, S, H, D] tensors (this build's extension), same values as BHSD:
+    the result equals the BHSD run bit for bit and meets the bar."""
+    log(f"[case] BSHD B={B} Hq={Hq} Hkv={Hkv} S={S} D={D} causal={causal} {dtype}")
+    g = O.golden(B, Hq, Hkv, S, D, causal, dtype=dtype)
+    res = run_v2(g, torch, bshd=True)
+    assert res["status"] == F.SUCCESS, F.status_name(res["status"])
+    check(res, g)
+    ref = run_v2(g, torch)
+    for n in ("dq", "dk", "dv", "delta"):
+        np.testing.assert_array_equal(res[n], ref[n])

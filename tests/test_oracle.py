@@ -26,7 +26,7 @@ torch = pytest.importorskip("torch")
 
 def torch_reference(g):
     """fp64 autograd of L = sum(dO * O) with O = softmax(scale*QK^T + mask) V."""
-    q, k, v, do = (torch.tensor(g[n].astype(np.float64), requires_grad=(n != "dout"))
+    q, k, v, do = (torch.tensor(O.to_f32(g[n]).astype(np.float64), requires_grad=(n != "dout"))
                    for n in ("q", "k", "v", "dout"))
     B, Hq, S, D = q.shape
     G = Hq // k.shape[1]
@@ -59,6 +59,45 @@ def test_oracle_matches_fp64_autograd(B, Hq, Hkv, S, D, causal):
     assert rel(g["dv"], t["dv"]) < 1e-5
     assert rel(g["dq"], t["dq"]) < 2e-3
     assert rel(g["dk"], t["dk"]) < 2e-3
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,causal", [(1, 2, 1, 32, 16, True), (1, 2, 2, 128, 64, False),
+                                                 (1, 1, 1, 128, 128, True)])
+def test_oracle_bf16_matches_fp64_autograd(B, Hq, Hkv, S, D, causal):
+    """bf16 tensors: same formulas, bf16 rounding of the inputs (taken as
+    exact here) and of O, whose 2^-9 relative error now dominates dQ / dK."""
+    g = O.golden(B, Hq, Hkv, S, D, causal, dtype="bf16")
+    assert g["q"].dtype == np.uint16 and g["out"].dtype == np.uint16
+    t = torch_reference(g)
+    assert rel(g["lse"], t["lse"]) < 1e-6
+    assert rel(O.to_f32(g["out"]), t["out"]) < 8e-3
+    assert rel(g["dv"], t["dv"]) < 1e-5
+    assert rel(g["dq"], t["dq"]) < 2e-2
+    assert rel(g["dk"], t["dk"]) < 2e-2
+
+
+def test_bf16_conversion_against_torch():
+    """bf16 <-> fp32 of the oracle against torch's conversions: every bf16
+    value, midpoints between neighbours (ties to even), random floats,
+    infinities and NaN."""
+    bits = np.arange(65536, dtype=np.uint16)
+    f = np.empty(65536, np.float32)
+    O.lib().fa3o_bf16_to_f32(bits, f, bits.size)
+    ref = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).float().numpy()
+    same = (f.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(f) & np.isnan(ref))
+    assert same.all()
+    finite = np.unique(ref[np.isfinite(ref)])
+    mids = ((finite[:-1].astype(np.float64) + finite[1:]) / 2).astype(np.float32)
+    rng = np.random.default_rng(1)
+    samples = np.concatenate([finite, mids, rng.standard_normal(100000).astype(np.float32) * 1e3,
+                              np.array([np.inf, -np.inf, 3.4e38, -1e-40, 1e-45], np.float32)])
+    out = np.empty(samples.size, np.uint16)
+    O.lib().fa3o_f32_to_bf16(np.ascontiguousarray(samples), out, samples.size)
+    want = torch.from_numpy(samples).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(out, want)
+    nan = np.array([np.nan], np.float32)
+    O.lib().fa3o_f32_to_bf16(nan, out[:1], 1)
+    assert np.isnan(O.bf16_to_f32(out[:1]))[0]
 
 
 def test_oracle_matches_finite_differences():
