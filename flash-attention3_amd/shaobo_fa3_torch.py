@@ -45,9 +45,11 @@ def _check(dout, q, k, v, out, lse):
         raise ValueError("k / v shape does not match q")
     if lse.shape != (B, Hq, S) or lse.dtype != torch.float32:
         raise ValueError("softmax_lse must be fp32 [B, Hq, S]")
-    for t in (dout, q, k, v, out):
-        if t.dtype != torch.float16:
-            raise ValueError("q, k, v, out, dout must be fp16")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("q, k, v, out, dout must be fp16 or bf16")
+    for t in (dout, k, v, out):
+        if t.dtype != q.dtype:
+            raise ValueError("q, k, v, out, dout must share one dtype")
     for t in (dout, q, k, v, out, lse):
         if not t.is_contiguous():
             raise ValueError("tensors must be contiguous (BHSD)")
@@ -62,12 +64,14 @@ def flash_attn_backward(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v:
                         softmax_scale: Optional[float] = None, deterministic: bool = False
                         ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """(dQ, dK, dV, softmax_d) of softmax(scale Q K^T) V given dO, O and the
-    natural-log LSE; fp16 BHSD in and out, softmax_d fp32 [B, Hq, S]."""
+    natural-log LSE; fp16 or bf16 BHSD in and out, softmax_d fp32 [B, Hq, S]."""
     _check(dout, q, k, v, out, softmax_lse)
     lib = _lib()
     B, Hq, S, D = q.shape
     p = F.make_params(lib, batch=B, seqlen=S, heads_q=Hq, heads_kv=k.shape[1], head_dim=D,
                       causal=causal, softmax_scale=softmax_scale, deterministic=deterministic)
+    if q.dtype == torch.bfloat16:
+        p.dtype = F.DTYPE_BF16
     nbytes = lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
     if nbytes == 0:
         raise RuntimeError("shaobo_fa3_bwd_v2: " +
@@ -105,7 +109,7 @@ def reference_forward(q, k, v, causal, scale):
         s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool, device=q.device), 1),
                           float("-inf"))
     lse = torch.logsumexp(s, dim=-1)
-    out = torch.matmul(torch.softmax(s, dim=-1), vf).half()
+    out = torch.matmul(torch.softmax(s, dim=-1), vf).to(q.dtype)
     return out.contiguous(), lse.contiguous()
 
 
@@ -126,6 +130,6 @@ class _Attention(torch.autograd.Function):
 
 
 def attention(q, k, v, causal=True, softmax_scale=None):
-    """softmax(scale Q K^T) V with the MI355X FA3 backward (fp16 BHSD)."""
+    """softmax(scale Q K^T) V with the MI355X FA3 backward (fp16 / bf16 BHSD)."""
     scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else softmax_scale
     return _Attention.apply(q, k, v, causal, scale)

@@ -92,6 +92,16 @@ def test_op_in_captured_graph():
             np.testing.assert_array_equal(a.cpu().numpy(), b.numpy(), err_msg=f"replay {i}")
 
 
+def test_op_bf16():
+    log("[case] torch op bf16")
+    g = O.golden(1, 4, 2, 512, 128, True, dtype="bf16")
+    dq, dk, dv, delta = op(inputs(g), True, g["scale"])
+    torch.cuda.synchronize()
+    assert dq.dtype == torch.bfloat16
+    check({"dq": dq.float().cpu().numpy(), "dk": dk.float().cpu().numpy(),
+           "dv": dv.float().cpu().numpy(), "delta": delta.cpu().numpy()}, g)
+
+
 def test_autograd_attention():
     """attention(): torch forward, library backward; gradients against fp32
     torch autograd of the same forward."""

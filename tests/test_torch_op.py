@@ -23,6 +23,13 @@ def test_op_is_registered():
     assert hasattr(torch.ops.shaobo_fa3, "flash_attn_backward")
 
 
+def test_fake_shapes_bf16():
+    with FakeTensorMode():
+        args = tensors(dtype=torch.bfloat16)
+        dq, dk, dv, delta = torch.ops.shaobo_fa3.flash_attn_backward(*args, False, 0.1, False)
+        assert dq.dtype == torch.bfloat16 and dk.shape == args[2].shape
+
+
 def test_fake_shapes():
     with FakeTensorMode():
         dout, q, k, v, out, lse = tensors()
@@ -38,7 +45,7 @@ def test_fake_rejects_bad_arguments(bad):
     with FakeTensorMode():
         dout, q, k, v, out, lse = tensors()
         if bad == "dtype":
-            q = q.to(torch.bfloat16)
+            q = q.to(torch.bfloat16)  # mixed with fp16 k / v / out / dout
         elif bad == "lse_shape":
             lse = lse[:, :, :128]
         elif bad == "heads":
