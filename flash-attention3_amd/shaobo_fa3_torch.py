@@ -10,7 +10,7 @@ correctly with the surrounding torch work and with CUDA-graph capture of
 that stream.  A fake (meta) implementation gives shapes for tracing.
 
 ``attention`` wraps it in an autograd function whose forward is a plain
-torch computation (O and the natural-log LSE in fp32, rounded O to fp16) --
+torch computation (O and the natural-log LSE in fp32, O rounded to the inputs' dtype) --
 an integration example and a test vehicle; the library provides the
 backward only.
 """
@@ -99,7 +99,7 @@ def _(dout, q, k, v, out, softmax_lse, causal, softmax_scale=None, deterministic
 
 
 def reference_forward(q, k, v, causal, scale):
-    """O (fp16) and natural-log LSE (fp32) in fp32 torch math."""
+    """O (the inputs' dtype) and natural-log LSE (fp32) in fp32 torch math."""
     G = q.shape[1] // k.shape[1]
     kf = k.float().repeat_interleave(G, dim=1)
     vf = v.float().repeat_interleave(G, dim=1)
