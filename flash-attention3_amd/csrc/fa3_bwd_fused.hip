@@ -491,17 +491,27 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
     // Cursor of the next query tile to load; a finished stream keeps
     // re-loading its last tile (into a stage nobody reads), so every step
     // issues the same loads.  All eight waves take part in every load.
-    int ld_h = hkv * group, ld_qt = qa, ld_left = n_it;
+    // (the cursor keeps running element and statistics-row offsets, so a
+    // step's issue is a few adds)
+    int ld_qt = qa, ld_left = n_it;
+    const int h0 = hkv * group;
+    size_t ld_e = q_elem<D>(a, b, h0, qa * 64);                  // Q / dO element
+    size_t ld_row = ((size_t)b * a.heads_q + h0) * S + qa * 64;  // statistics row
+    const size_t step_e = (size_t)64 * a.q_rs;
+    const size_t wrap_e = (size_t)a.q_hs - (size_t)(qb - qa - 1) * step_e;  // next head, tile qa
+    const size_t wrap_row = (size_t)S - (size_t)(qb - qa - 1) * 64;
     auto issue = [&](FA3_LDS char* st) {
-        const size_t row0 = ((size_t)b * a.heads_q + ld_h) * S + ld_qt * 64;  // statistics row
-        const size_t e0 = q_elem<D>(a, b, ld_h, ld_qt * 64);
-        load_tile_async<D>(st, a.q + e0, ld_off, w);
-        load_tile_async<D>(st + C::kTileBytes, a.dout + e0, ld_off, w);
-        load_rows_async<kRows>(st + 2 * C::kTileBytes, a, row0, w, lane);
+        load_tile_async<D>(st, a.q + ld_e, ld_off, w);
+        load_tile_async<D>(st + C::kTileBytes, a.dout + ld_e, ld_off, w);
+        load_rows_async<kRows>(st + 2 * C::kTileBytes, a, ld_row, w, lane);
         if (--ld_left > 0) {
             if (++ld_qt == qb) {
                 ld_qt = qa;
-                ++ld_h;
+                ld_e += wrap_e;
+                ld_row += wrap_row;
+            } else {
+                ld_e += step_e;
+                ld_row += 64;
             }
         }
     };
@@ -784,11 +794,15 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
     const _Float16* kh = a.k + kv_elem<D>(a, b, hkv, 0);
     const _Float16* vh = a.v + kv_elem<D>(a, b, hkv, 0);
     int ld_kt = ka;
+    size_t ld_e = (size_t)ka * 64 * a.kv_rs;
+    const size_t step_e = (size_t)64 * a.kv_rs;
     auto issue = [&](FA3_LDS char* st) {
-        const size_t e = (size_t)ld_kt * 64 * a.kv_rs;
-        load_tile_async<D>(st, kh + e, ld_off, w);
-        load_tile_async<D>(st + C::kTileBytes, vh + e, ld_off, w);
-        if (ld_kt + 1 < kb) ++ld_kt;
+        load_tile_async<D>(st, kh + ld_e, ld_off, w);
+        load_tile_async<D>(st + C::kTileBytes, vh + ld_e, ld_off, w);
+        if (ld_kt + 1 < kb) {
+            ++ld_kt;
+            ld_e += step_e;
+        }
     };
     auto top = [&]() {
         wait_vm_lgkm0<C::kDmaQ>();
