@@ -324,16 +324,61 @@ __device__ __forceinline__ int dkv_pair(int t, int u) {
     return 2 * ((D / 64) * (t & 1) + u) + (t >> 1);
 }
 
+// Byte offset of 16-byte chunk c (of 4) of row r in a [rows][32] fp16
+// staging tile (64-byte rows, chunks XOR-swizzled by r / 4): 16 rows x 4
+// chunks read with ds_read_b128 and 32 rows x 8 bytes written with
+// ds_write_b64 are both bank-conflict free.
+__device__ __forceinline__ uint32_t row64_off(int r, int c) {
+    return (uint32_t)(r * 64 + ((c ^ (r >> 2)) & 3) * 16);
+}
+
 // dV^T / dK^T accumulators of gradient wave t (pairs dkv_pair(t, u)) to dV /
 // dK of KV head bkv, keys kbase ..; lane: key 32 kb + l32,
-// d = 32 slice + 8 (i / 4) + 4 h + i % 4.
+// d = 32 slice + 8 (i / 4) + 4 h + i % 4.  The wave's pairs share one matrix
+// and cover D columns d0 .. d0 + 32 kPpw of all 64 keys; 16-bit outputs are
+// transposed through the wave's own 8 KiB (D 64: 4 KiB) of `stage` so that
+// every global store writes whole 128-byte (D 64: 64-byte) row segments.
 template <int D, bool kBf16>
 __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase, int t, int lane,
-                                          const f32x16 (&acc)[D / 64][2]) {
+                                          const f32x16 (&acc)[D / 64][2], FA3_LDS char* stage) {
     constexpr int kPpw = D / 64;
     const int l32 = lane & 31, h = lane >> 5;
     const int b = bkv / a.heads_kv;
     const size_t base = kv_elem<D>(a, b, bkv - b * a.heads_kv, kbase);
+    if (!a.out_f32) {
+        const float mul = (t >> 1) == 0 ? 1.f : a.scale;
+        _Float16* outp = (_Float16*)((t >> 1) == 0 ? a.dv : a.dk);
+        const int d0 = 32 * kPpw * (t & 1);
+        FA3_LDS char* st = stage + t * (64 * 64 * kPpw);
+#pragma unroll
+        for (int u = 0; u < kPpw; ++u)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4) {
+                    f16x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = to16<kBf16>(acc[u][kb][4 * a4 + e] * mul);
+                    const int key = 32 * kb + l32;
+                    const uint32_t off = D == 128 ? dst_off(key, 4 * u + a4) : row64_off(key, a4);
+                    lds_write_b64(st, off + 8 * h, v);
+                }
+        // the wave reads back only what it wrote: its LDS accesses complete in order
+#pragma unroll
+        for (int j = 0; j < 8 * kPpw / 2; ++j) {
+            int key, c;
+            if constexpr (D == 128) {
+                key = 8 * j + ((lane >> 2) & 7);
+                c = (lane & 3) | ((lane >> 5) << 2);
+            } else {
+                key = 16 * j + (lane >> 2);
+                c = lane & 3;
+            }
+            const f16x8 x = lds_read_b128(st, D == 128 ? dst_off(key, c) : row64_off(key, c));
+            *(f16x8*)(outp + base + (size_t)key * a.kv_rs + d0 + 8 * c) = x;
+        }
+        return;
+    }
 #pragma unroll
     for (int u = 0; u < kPpw; ++u) {
         const int pu = dkv_pair<D>(t, u);
@@ -354,14 +399,36 @@ __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase
 }
 
 // dQ^T accumulators of gradient wave t to the dQ tile at element `base`;
-// lane: row 32 rb + l32, d = 32 db + 8 (i / 4) + 4 h + i % 4.
+// lane: row 32 rb + l32, d = 32 db + 8 (i / 4) + 4 h + i % 4.  16-bit
+// outputs go through the wave's 4 KiB (D 64: 2 KiB) of `stage`, so every
+// global store writes whole 64-byte row segments.
 template <int D, bool kBf16>
 __device__ __forceinline__ void store_dq(const FusedArgs& a, size_t base, int t, int lane,
-                                         const f32x16 (&acc)[D / 64]) {
+                                         const f32x16 (&acc)[D / 64], FA3_LDS char* stage) {
     constexpr int kRb = D / 64;
     const int db = D == 128 ? t : t >> 1;
     const int rb0 = D == 128 ? 0 : t & 1;
     const int l32 = lane & 31, h = lane >> 5;
+    if (!a.out_f32) {
+        FA3_LDS char* st = stage + t * (32 * kRb * 64);
+#pragma unroll
+        for (int r = 0; r < kRb; ++r)
+#pragma unroll
+            for (int a4 = 0; a4 < 4; ++a4) {
+                f16x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = to16<kBf16>(acc[r][4 * a4 + e] * a.scale);
+                lds_write_b64(st, row64_off(32 * r + l32, a4) + 8 * h, v);
+            }
+        _Float16* outp = (_Float16*)a.dq + base + 32 * db;
+#pragma unroll
+        for (int j = 0; j < 2 * kRb; ++j) {
+            const int r = 16 * j + (lane >> 2), c = lane & 3;  // r: row within the wave's block
+            const f16x8 x = lds_read_b128(st, row64_off(r, c));
+            *(f16x8*)(outp + (size_t)(32 * rb0 + r) * a.q_rs + 8 * c) = x;
+        }
+        return;
+    }
     const size_t off0 = base + 32 * db + 4 * h;
 #pragma unroll
     for (int r = 0; r < kRb; ++r) {
@@ -745,8 +812,11 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         } else {
             last(xa, pds0);
         }
+        // st_1 is free now: nobody reads it any more, and only the latest
+        // issue (into st_ld, or st_2 after a rotate) may still be landing, so
+        // it stages the outputs
         if (slot < 0) {
-            store_dkv<D, kBf16>(a, bkv, kbase, t, lane, acc);
+            store_dkv<D, kBf16>(a, bkv, kbase, t, lane, acc, st_1);
             return;
         }
         // partial sums: [piece][wave][2 kPpw accumulator blocks]
@@ -757,7 +827,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         if (split_end(a.counters + a.cnt_kv + (slot >> 1), flag,
                       [&] { put_partials<kBlk>(pr, part(slot), flat, lane); })) {
             add_partials<kBlk>(pr, part(slot ^ 1), flat, lane);
-            store_dkv<D, kBf16>(a, bkv, kbase, t, lane, acc);
+            store_dkv<D, kBf16>(a, bkv, kbase, t, lane, acc, st_1);
         }
     }
 }
@@ -994,8 +1064,9 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         } else {
             last(xa, ds0);
         }
+        // st_1 is free now (see dkv_role) and stages the outputs
         if (slot < 0) {
-            store_dq<D, kBf16>(a, q0, t, lane, acc);
+            store_dq<D, kBf16>(a, q0, t, lane, acc, st_1);
             return;
         }
         // partial sums: [piece][wave][kRb accumulator blocks]
@@ -1004,7 +1075,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         if (split_end(a.counters + a.cnt_q + (slot >> 1), flag,
                       [&] { put_partials<kRb>(pr, part(slot), acc, lane); })) {
             add_partials<kRb>(pr, part(slot ^ 1), acc, lane);
-            store_dq<D, kBf16>(a, q0, t, lane, acc);
+            store_dq<D, kBf16>(a, q0, t, lane, acc, st_1);
         }
     }
 }
