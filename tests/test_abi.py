@@ -8,8 +8,8 @@
 * Differential check of shaobo_fa3_bwd_v2_validate against the reference's
   own validation code compiled from its sources (oracle/_ref/libref_api.so,
   reference src/shaobo_fa3_bwd_api.cpp:53-120) over thousands of random
-  parameter structs.  The only allowed difference is this build's head_dim 64
-  extension.
+  parameter structs.  The only allowed differences are this build's
+  extensions: head_dim 64, BF16 and BSHD.
 * Workspace sizing and the error paths of the launch entries that return
   before any HIP call.
 """
