@@ -117,10 +117,18 @@ struct Cfg {
     static constexpr int kKs = D / 32;                      // 16x16x32 k-steps over D
     static constexpr int kDB = D / 32;                      // 32-wide slices of D
     static constexpr int kChunks = D / 8;                   // 16-byte chunks per row
-    static constexpr int kLoadsPerTile = kTileBytes / (kWaves * 1024);  // per lane
-    // direct-to-LDS loads per wave and stage: dKV Q, dO, rows; dQ K, V
-    static constexpr int kDmaKv = 2 * kLoadsPerTile + 1;
-    static constexpr int kDmaQ = 2 * kLoadsPerTile;
+    static constexpr int kLoadsPerTile = kTileBytes / (kWaves * 1024);  // per lane, 8 loaders
+    // Who issues the streamed tiles' loads: at D 64 the 4 gradient waves
+    // (their MFMAs wait for the score waves' anyway, and the score waves are
+    // the step's critical path: P5 -9 %); at D 128 all 8 waves (a gradient
+    // wave with twice the loads and the larger transposed reads becomes the
+    // critical path: P3 +7 %).
+    static constexpr bool kGradLoads = D == 64;
+    static constexpr int kLoaders = kGradLoads ? 4 : 8;
+    static constexpr int kNld = kTileBytes / (kLoaders * 1024);  // tile loads per loader
+    // direct-to-LDS loads per loading wave and stage: dKV Q, dO, rows; dQ K, V
+    static constexpr int kDmaKv = 2 * kNld + 1;
+    static constexpr int kDmaQ = 2 * kNld;
     // phase-2 split: the dKV role has 2 * kDB (matrix, D-slice) pairs, the dQ
     // role kDB D-slices; the 8 waves cover them with kSplitKv / kSplitQ waves
     // each, splitting the 4 contraction steps of a tile between them.
@@ -181,16 +189,17 @@ __device__ __forceinline__ _Float16 to16(float x) {
 }
 
 // Direct-to-LDS copy of a row-major [64][D] fp16 tile into a swizzled LDS
-// tile.  Lane `lane` of wave `wave` moves the 16-byte chunk that belongs at
-// LDS byte blk * 1024 + lane * 16 (blk = wave * kLoadsPerTile + j); its
-// source byte offset within the global tile is precomputed once.
-template <int D>
-__device__ __forceinline__ void tile_load_offsets(uint32_t (&off)[Cfg<D>::kLoadsPerTile],
-                                                  int wave, int lane, int row_stride) {
+// tile, shared by loaders (waves) of N 1 KiB blocks each.  Lane `lane` of
+// loader `ld` moves the 16-byte chunk that belongs at LDS byte
+// blk * 1024 + lane * 16 (blk = ld * N + j); its source byte offset within the
+// global tile is precomputed once.
+template <int D, int N = Cfg<D>::kLoadsPerTile>
+__device__ __forceinline__ void tile_load_offsets(uint32_t (&off)[N], int ld, int lane,
+                                                  int row_stride) {
     using C = Cfg<D>;
 #pragma unroll
-    for (int j = 0; j < C::kLoadsPerTile; ++j) {
-        const int id = (wave * C::kLoadsPerTile + j) * 64 + lane;  // physical chunk
+    for (int j = 0; j < N; ++j) {
+        const int id = (ld * N + j) * 64 + lane;  // physical chunk
         const int row = id / C::kChunks;
         const int phys = id % C::kChunks;
         int sw;
@@ -201,16 +210,36 @@ __device__ __forceinline__ void tile_load_offsets(uint32_t (&off)[Cfg<D>::kLoads
     }
 }
 
-template <int D>
+template <int N>
 __device__ __forceinline__ void load_tile_async(FA3_LDS char* tile, const _Float16* src,
-                                                const uint32_t (&off)[Cfg<D>::kLoadsPerTile],
-                                                int wave) {
-    using C = Cfg<D>;
+                                                const uint32_t (&off)[N], int ld) {
 #pragma unroll
-    for (int j = 0; j < C::kLoadsPerTile; ++j) {
+    for (int j = 0; j < N; ++j) {
         __builtin_amdgcn_global_load_lds((const void*)((const char*)src + off[j]),
-                                         (FA3_LDS void*)(tile + (wave * C::kLoadsPerTile + j) * 1024),
-                                         16, 0, 0);
+                                         (FA3_LDS void*)(tile + (ld * N + j) * 1024), 16, 0, 0);
+    }
+}
+
+// Direct-to-LDS copy of the statistics of the 64 query rows row0 .. of a
+// streamed tile by the 4 gradient waves, loader t moving rows 16 t .. 16 t +
+// 15 (one load each; one dword per active lane):
+//   kRows 0: lse2 -> rows[32 t .. 32 t + 16), -delta -> rows[32 t + 16 ..
+//            32 t + 32) (lanes 0..31);
+//   kRows 1: packed[3 (row0 + 16 t) ..] -> rows[48 t .. 48 t + 48), i.e. the
+//            [row][3] layout of all 64 rows (lanes 0..47).
+template <int kRows>
+__device__ __forceinline__ void load_rows4_async(FA3_LDS char* rows, const FusedArgs& a,
+                                                 size_t row0, int t, int lane) {
+    if constexpr (kRows == 0) {
+        const float* src = (lane < 16 ? a.lse2 : a.ndelta) + row0 + 16 * t + (lane & 15);
+        if (lane < 32)
+            __builtin_amdgcn_global_load_lds((const void*)src, (FA3_LDS void*)(rows + 128 * t), 4,
+                                             0, 0);
+    } else {
+        static_assert(kRows == 1, "per-step rows of the dKV role");
+        if (lane < 48)
+            __builtin_amdgcn_global_load_lds((const void*)(a.packed + 3 * (row0 + 16 * t) + lane),
+                                             (FA3_LDS void*)(rows + 192 * t), 4, 0, 0);
     }
 }
 
@@ -551,15 +580,17 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
     const int kbase = kt * 64;
     const int n_it = group * (qb - qa);
 
-    uint32_t ld_off[C::kLoadsPerTile], kv_off[C::kLoadsPerTile];
-    tile_load_offsets<D>(ld_off, w, lane, a.q_rs);
+    // loader index of this wave when it loads (see Cfg::kGradLoads)
+    const int ldr = C::kGradLoads ? t : w;
+    const bool loads = !C::kGradLoads || w >= 4;
+    uint32_t ld_off[C::kNld], kv_off[C::kLoadsPerTile];
+    tile_load_offsets<D, C::kNld>(ld_off, ldr, lane, a.q_rs);
     tile_load_offsets<D>(kv_off, w, lane, a.kv_rs);
 
     // Cursor of the next query tile to load; a finished stream keeps
     // re-loading its last tile (into a stage nobody reads), so every step
-    // issues the same loads.  All eight waves take part in every load.
-    // (the cursor keeps running element and statistics-row offsets, so a
-    // step's issue is a few adds)
+    // issues the same loads.  (The cursor keeps running element and
+    // statistics-row offsets, so a step's issue is a few adds.)
     int ld_qt = qa, ld_left = n_it;
     const int h0 = hkv * group;
     size_t ld_e = q_elem<D>(a, b, h0, qa * 64);                  // Q / dO element
@@ -567,10 +598,13 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
     const size_t step_e = (size_t)64 * a.q_rs;
     const size_t wrap_e = (size_t)a.q_hs - (size_t)(qb - qa - 1) * step_e;  // next head, tile qa
     const size_t wrap_row = (size_t)S - (size_t)(qb - qa - 1) * 64;
-    auto issue = [&](FA3_LDS char* st) {
-        load_tile_async<D>(st, a.q + ld_e, ld_off, w);
-        load_tile_async<D>(st + C::kTileBytes, a.dout + ld_e, ld_off, w);
-        load_rows_async<kRows>(st + 2 * C::kTileBytes, a, ld_row, w, lane);
+    auto issue = [&](FA3_LDS char* st) {  // loading waves
+        load_tile_async(st, a.q + ld_e, ld_off, ldr);
+        load_tile_async(st + C::kTileBytes, a.dout + ld_e, ld_off, ldr);
+        if constexpr (C::kGradLoads)
+            load_rows4_async<kRows>(st + 2 * C::kTileBytes, a, ld_row, t, lane);
+        else
+            load_rows_async<kRows>(st + 2 * C::kTileBytes, a, ld_row, w, lane);
         if (--ld_left > 0) {
             if (++ld_qt == qb) {
                 ld_qt = qa;
@@ -582,8 +616,12 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
             }
         }
     };
+    // Step barrier: the loading waves' loads of the next tile have landed
+    // (only the latest issue may be in flight) and every wave's LDS accesses
+    // are done.
     auto top = [&]() {
-        wait_vm_lgkm0<C::kDmaKv>();
+        if (loads) wait_vm_lgkm0<C::kDmaKv>();
+        else wait_vm_lgkm0<0>();
         barrier();
     };
 
@@ -602,12 +640,16 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
     auto prologue_loads = [&]() {
         // this key tile's K and V are staged in the P / dS area
         const size_t k0 = kv_elem<D>(a, b, hkv, kbase);
-        load_tile_async<D>(pds0, a.k + k0, kv_off, w);
-        load_tile_async<D>(pds0 + C::kTileBytes, a.v + k0, kv_off, w);
-        issue(st_ld);
-        issue(st_1);
-        issue(st_2);
-        wait_vm_lgkm0<2 * C::kDmaKv>();
+        load_tile_async(pds0, a.k + k0, kv_off, w);
+        load_tile_async(pds0 + C::kTileBytes, a.v + k0, kv_off, w);
+        if (loads) {
+            issue(st_ld);
+            issue(st_1);
+            issue(st_2);
+            wait_vm_lgkm0<2 * C::kDmaKv>();
+        } else {
+            wait_vm_lgkm0<0>();
+        }
         barrier();
     };
 
@@ -636,9 +678,12 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
             }
             f32x4 l2, ndl;  // lse2 and -delta of rows 16 t + 4 g4 + i
             if constexpr (kRows == 0) {
-                const FA3_LDS char* r = st + 2 * C::kTileBytes + (16 * t + 4 * g4) * 4;
+                // lse2 / -delta of rows 16 t .. in the layout of the loaders
+                const FA3_LDS char* r =
+                    st + 2 * C::kTileBytes +
+                    (C::kGradLoads ? 128 * t + 16 * g4 : (16 * t + 4 * g4) * 4);
                 l2 = *(const FA3_LDS f32x4*)r;
-                ndl = *(const FA3_LDS f32x4*)(r + 256);
+                ndl = *(const FA3_LDS f32x4*)(r + (C::kGradLoads ? 64 : 256));
             } else {
                 // [row][max_log2, inv_sum, delta]: exp2(x - m) * inv = exp2(x - (m - log2 inv))
                 const FA3_LDS f32x4* r =
@@ -703,14 +748,15 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                     kf[kb][s] = lds_read_b128(pa, off);
                     vf[kb][s] = lds_read_b128(pa + C::kTileBytes, off);
                 }
-            wait_vm_lgkm0<2 * C::kDmaKv>();  // K / V reads done before P / dS overwrite them
+            if constexpr (C::kGradLoads) wait_vm_lgkm0<0>();  // K / V reads done before P / dS overwrite them
+            else wait_vm_lgkm0<2 * C::kDmaKv>();
             barrier();
             score(next_masked(), s0, pa);
         };
         auto step = [&](FA3_LDS char* __restrict__ ld, const FA3_LDS char* __restrict__ s1,
                         FA3_LDS char* __restrict__ pwr) {
             top();
-            issue(ld);
+            if constexpr (!C::kGradLoads) issue(ld);
             __builtin_amdgcn_sched_barrier(0);
             score(next_masked(), s1, pwr);
             __builtin_amdgcn_sched_barrier(0);
@@ -858,24 +904,27 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
     const size_t q0 = q_elem<D>(a, b, hq, qt * 64);  // this tile's Q / dO / dQ elements
     const int n_kt = kb - ka;
 
-    uint32_t ld_off[C::kLoadsPerTile], q_off[C::kLoadsPerTile];
-    tile_load_offsets<D>(ld_off, w, lane, a.kv_rs);
+    const int ldr = C::kGradLoads ? t : w;  // as in dkv_role
+    const bool loads = !C::kGradLoads || w >= 4;
+    uint32_t ld_off[C::kNld], q_off[C::kLoadsPerTile];
+    tile_load_offsets<D, C::kNld>(ld_off, ldr, lane, a.kv_rs);
     tile_load_offsets<D>(q_off, w, lane, a.q_rs);
     const _Float16* kh = a.k + kv_elem<D>(a, b, hkv, 0);
     const _Float16* vh = a.v + kv_elem<D>(a, b, hkv, 0);
     int ld_kt = ka;
     size_t ld_e = (size_t)ka * 64 * a.kv_rs;
     const size_t step_e = (size_t)64 * a.kv_rs;
-    auto issue = [&](FA3_LDS char* st) {
-        load_tile_async<D>(st, kh + ld_e, ld_off, w);
-        load_tile_async<D>(st + C::kTileBytes, vh + ld_e, ld_off, w);
+    auto issue = [&](FA3_LDS char* st) {  // loading waves
+        load_tile_async(st, kh + ld_e, ld_off, ldr);
+        load_tile_async(st + C::kTileBytes, vh + ld_e, ld_off, ldr);
         if (ld_kt + 1 < kb) {
             ++ld_kt;
             ld_e += step_e;
         }
     };
     auto top = [&]() {
-        wait_vm_lgkm0<C::kDmaQ>();
+        if (loads) wait_vm_lgkm0<C::kDmaQ>();
+        else wait_vm_lgkm0<0>();
         barrier();
     };
 
@@ -894,13 +943,17 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
     auto prologue_loads = [&]() {
         // this query tile's Q and dO are staged in the dS area, its lse2 and
         // -delta in the (otherwise unused) rows slot of stage 0
-        load_tile_async<D>(ds0, a.q + q0, q_off, w);
-        load_tile_async<D>(ds0 + C::kTileBytes, a.dout + q0, q_off, w);
+        load_tile_async(ds0, a.q + q0, q_off, w);
+        load_tile_async(ds0 + C::kTileBytes, a.dout + q0, q_off, w);
         load_rows_async<kRows>(st_ld + 2 * C::kTileBytes, a, row0, w, lane);
-        issue(st_ld);
-        issue(st_1);
-        issue(st_2);
-        wait_vm_lgkm0<2 * C::kDmaQ>();
+        if (loads) {
+            issue(st_ld);
+            issue(st_1);
+            issue(st_2);
+            wait_vm_lgkm0<2 * C::kDmaQ>();
+        } else {
+            wait_vm_lgkm0<0>();
+        }
         barrier();
     };
 
@@ -971,7 +1024,8 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
                 }
                 ndl[rb] = f32x4{n, n, n, n};
             }
-            wait_vm_lgkm0<2 * C::kDmaQ>();  // Q / dO reads done before dS overwrites them
+            if constexpr (C::kGradLoads) wait_vm_lgkm0<0>();  // Q / dO reads done before dS overwrites them
+            else wait_vm_lgkm0<2 * C::kDmaQ>();
             barrier();
             score(kCausal && ka == qt, s0, pa);
         };
@@ -979,7 +1033,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         auto step = [&](bool masked, FA3_LDS char* __restrict__ ld,
                         const FA3_LDS char* __restrict__ s1, FA3_LDS char* __restrict__ pwr) {
             top();
-            issue(ld);
+            if constexpr (!C::kGradLoads) issue(ld);
             __builtin_amdgcn_sched_barrier(0);
             score(masked, s1, pwr);
             __builtin_amdgcn_sched_barrier(0);
