@@ -524,35 +524,52 @@ __device__ __forceinline__ void add_partials(__amdgpu_buffer_rsrc_t r, uint32_t 
 // their partial sums, the score waves with a no-op -- and it returns true in
 // every wave when this workgroup is to write the job's output.
 //
-// Score wave 0 has already peeked at the job's arrival counter into *flag
-// (right after its last barrier, while the gradient waves ran the last
-// products).  If the other piece had arrived, its partial sums are complete
-// and visible, so this piece adds them to its registers and needs no partial
-// of its own.  Otherwise it stores its partial sums, waits until every wave's
-// stores have completed, and counts its arrival; the piece that arrives
-// second then adds the other piece's partial sums.  Either way the output is
-// piece 0 + piece 1 (a two-term sum is the same in either order), so the
-// result does not depend on which piece finishes first.  The counters are
-// cleared by the preprocess kernel before every launch.
-template <typename PutOwn>
-__device__ __forceinline__ bool split_end(int* counter, FA3_LDS int* flag, PutOwn&& put_own) {
-    wait_vm_lgkm0<0>();
-    barrier();
-    if (*flag == 1) return true;
-    put_own();
-    wait_vm_lgkm0<0>();
-    barrier();
+// The job's counter (cleared by the preprocess kernel before every launch)
+// orders the two pieces.  Score wave 0 counts this piece's arrival
+// (split_arrive, +1) right after its last barrier, while the gradient waves
+// run the last products.  The piece that arrives first stores its partial
+// sums, waits until every wave's stores have completed and adds 2 to the
+// counter; it writes nothing else.  The piece that arrives second stores no
+// partials: it waits for that mark (counter 4; it saw 3 if the mark came
+// first) and adds the first piece's partial sums to its registers.  The
+// output is piece 0 + piece 1 either way (a two-term sum is the same in either
+// order), so the result does not depend on which piece finishes first.  The
+// wait cannot block for long: the first piece has arrived and only stores
+// and counts after that; the spin is bounded all the same.
+constexpr int kSplitSpinLimit = 1 << 24;
+
+__device__ __forceinline__ void split_arrive(int* counter, FA3_LDS int* flag) {
     if (threadIdx.x == 0)
         *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    wait_vm_lgkm0<0>();
-    barrier();
-    return *flag == 1;
 }
 
-__device__ __forceinline__ void split_peek(const int* counter, FA3_LDS int* flag) {
-    if (threadIdx.x == 0)
-        *flag = __hip_atomic_load(const_cast<int*>(counter), __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
+template <typename PutOwn>
+__device__ __forceinline__ bool split_end(const int* counter, FA3_LDS int* flag, PutOwn&& put_own) {
+    wait_vm_lgkm0<0>();
+    barrier();
+    const int seen = *flag;
+    if (seen == 0) {
+        put_own();
+        wait_vm_lgkm0<0>();
+        barrier();
+        if (threadIdx.x == 0)
+            __hip_atomic_fetch_add(const_cast<int*>(counter), 2, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+    }
+    if (seen != 3) {
+        if (threadIdx.x == 0) {
+            for (int i = 0; i < kSplitSpinLimit; ++i) {
+                if (__hip_atomic_load(const_cast<int*>(counter), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) >= 4)
+                    break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        wait_vm_lgkm0<0>();
+        barrier();
+    }
+    return true;
 }
 
 // ----------------------------------------------------------------------------
@@ -774,7 +791,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         top();  // matches the gradient waves' last phase
         if (slot >= 0) {
             int* counter = a.counters + a.cnt_kv + (slot >> 1);
-            split_peek(counter, flag);
+            split_arrive(counter, flag);
             split_end(counter, flag, [] {});
         }
     } else {
@@ -1051,7 +1068,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         top();  // matches the gradient waves' last phase
         if (slot >= 0) {
             int* counter = a.counters + a.cnt_q + (slot >> 1);
-            split_peek(counter, flag);
+            split_arrive(counter, flag);
             split_end(counter, flag, [] {});
         }
     } else {
@@ -1273,16 +1290,21 @@ void set_job_map(FusedArgs& a) {
 // Head-piece lengths of the split plan.  Workgroup times in units of one dKV
 // step, measured on MI355X at B1 H4 S2048 D128 (per-workgroup timestamps):
 // a dQ step costs 0.73, a unit's prologue (loads + first score phase) 2.5,
-// its epilogue 2.0 (dKV) / 0.8 (dQ) for a whole job, 2.6 / 1.6 for a head
-// piece that publishes its partial sums, 3.5 / 2.0 for the piece that adds
-// them; 0.65 at kernel entry and between two units.  For each x the pair of
+// its epilogue 2.0 (dKV) / 0.8 (dQ) for a whole job; of a split job, the
+// piece that arrives first spends kPub (storing its partial sums) and the
+// second, after waiting for them, kAdd (adding them and writing the output);
+// 0.65 at kernel entry and between two units.  For each x the pair of
 // workgroups sharing a job is balanced: the head length minimises the later
 // of the two finishing times.
 void split_heads(int M, uint16_t* head_kv, uint16_t* head_q) {
     constexpr double kQ = 0.73, kPro = 2.5, kEntry = 0.65, kGap = 0.65;
-    constexpr double kWholeKv = 2.0, kWholeQ = 0.8, kHeadKv = 2.6, kHeadQ = 1.6;
-    constexpr double kAddKv = 3.5, kAddQ = 2.0;
-    auto unit = [&](double step, int n, double epi) { return kPro + (n - 1) * step + epi; };
+    constexpr double kWholeKv = 2.0, kWholeQ = 0.8;
+    constexpr double kPubKv = 2.6, kAddKv = 2.8, kPubQ = 1.6, kAddQ = 1.8;
+    // a, b: the two workgroups' times up to the end of their last steps
+    auto pair_end = [](double a, double b, double pub, double add) {
+        const double first = a < b ? a : b, second = a < b ? b : a;
+        return (second > first + pub ? second : first + pub) + add;
+    };
     const int QT = 2 * M;
     for (int x = 0; x < M; ++x) {
         // dKV key tile x (QT - x tiles): head piece alone, remainder after
@@ -1291,10 +1313,10 @@ void split_heads(int M, uint16_t* head_kv, uint16_t* head_q) {
         double best_t = 1e30;
         for (int L = 1; L <= QT - x; ++L) {
             const int r = QT - x - L;
-            const double c = kEntry + unit(1.0, L, r > 0 ? kHeadKv : kWholeKv);
-            double b = kEntry + unit(kQ, x + 1, kWholeQ);
-            if (r > 0) b += kGap + unit(1.0, r, kAddKv);
-            const double t = c > b ? c : b;
+            const double c = kEntry + kPro + (L - 1);
+            const double b = kEntry + kPro + x * kQ + kWholeQ;
+            const double t = r > 0 ? pair_end(c, b + kGap + kPro + (r - 1), kPubKv, kAddKv)
+                                   : (c + kWholeKv > b ? c + kWholeKv : b);
             if (t < best_t) {
                 best_t = t;
                 best = L;
@@ -1307,10 +1329,10 @@ void split_heads(int M, uint16_t* head_kv, uint16_t* head_q) {
         best_t = 1e30;
         for (int L = 1; L <= M + x + 1; ++L) {
             const int r = M + x + 1 - L;
-            const double d = kEntry + unit(kQ, L, r > 0 ? kHeadQ : kWholeQ);
-            double av = kEntry + unit(1.0, M - x, kWholeKv);
-            if (r > 0) av += kGap + unit(kQ, r, kAddQ);
-            const double t = d > av ? d : av;
+            const double d = kEntry + kPro + (L - 1) * kQ;
+            const double av = kEntry + kPro + (M - x - 1) + kWholeKv;
+            const double t = r > 0 ? pair_end(d, av + kGap + kPro + (r - 1) * kQ, kPubQ, kAddQ)
+                                   : (d + kWholeQ > av ? d + kWholeQ : av);
             if (t < best_t) {
                 best_t = t;
                 best = L;
