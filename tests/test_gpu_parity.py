@@ -38,6 +38,12 @@ CASES = [
     (2, 8, 2, 256, 128, False),   # GQA G=4, batch 2, non-causal
     (1, 2, 2, 512, 64, True),     # D = 64
     (1, 2, 1, 384, 64, False),    # D = 64 GQA, S not a power of two
+    # split plan (causal, one query head per KV head, S / 64 even and >= 4):
+    (1, 1, 1, 256, 128, True),    # smallest: M = S / 128 = 2
+    (1, 3, 3, 384, 128, True),    # odd M = 3, 3 groups (no XCD-aligned map)
+    (2, 2, 2, 1024, 128, True),   # batch 2: 4 groups
+    (1, 5, 5, 640, 64, True),     # M = 5, D = 64
+    (1, 2, 2, 4096, 64, True),    # M = 32, D = 64
 ]
 
 
