@@ -33,17 +33,19 @@
 // barrier per step suffices; both loops pass the same barriers, and the
 // compiler allocates registers for the larger of the two, not their sum.
 // Every global read of the loop is a direct-to-LDS load (global_load_lds)
-// into one of three stages, issued two steps ahead: a stage holds a streamed
-// tile pair and, in the dKV role, its 64 rows' statistics.  The issue pattern
+// into one of three stages, issued two steps ahead (by all 8 waves at head
+// dim 128, by the gradient waves at 64): a stage holds a streamed tile pair
+// and, in the dKV role, its 64 rows' statistics.  The issue pattern
 // is the same every step (a finished stream re-loads its last tile into a
 // free stage), so every wait is a constant count.
 //
 // Split plan (causal, one query head per KV head, at most 512 jobs; see
 // bwd_fused_kernel): long jobs are cut in two pieces run by different
-// workgroups.  Each piece stores its fp32 partial sums with device-coherent
-// stores and then bumps an arrival counter; the piece that arrives second
-// adds piece 0 + piece 1 in that fixed order and writes the output, so the
-// result does not depend on which piece finished first.
+// workgroups.  Each piece counts its arrival; the first to arrive stores its
+// fp32 partial sums with device-coherent stores and marks them done, the
+// second waits for that mark, adds them to its own and writes the output.
+// fp32 addition of two terms is commutative, so the result does not depend
+// on which piece finished first.
 #include "fa3_bwd_device.h"
 #include "fa3_bwd_internal.h"
 
