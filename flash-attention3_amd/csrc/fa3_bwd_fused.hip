@@ -716,6 +716,9 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                     ndl[i] = -f[3 * i + 2];
                 }
             }
+            // all operand reads in flight before the first MFMA: the waits
+            // then count down instead of draining the LDS queue per k-step
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int s = 0; s < C::kKs; ++s) {
 #pragma unroll
@@ -993,6 +996,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
                 ak[s] = lds_read_b128(st, off);
                 av[s] = lds_read_b128(st + C::kTileBytes, off);
             }
+            __builtin_amdgcn_sched_barrier(0);  // as in dkv_role
 #pragma unroll
             for (int s = 0; s < C::kKs; ++s) {
 #pragma unroll
