@@ -661,11 +661,13 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         const size_t k0 = kv_elem<D>(a, b, hkv, kbase);
         load_tile_async(pds0, a.k + k0, kv_off, w);
         load_tile_async(pds0 + C::kTileBytes, a.v + k0, kv_off, w);
+        // wait for K and V only: the score waves copy them into registers
+        // while the first streamed tile lands (the prologues wait for it)
         if (loads) {
             issue(st_ld);
             issue(st_1);
             issue(st_2);
-            wait_vm_lgkm0<2 * C::kDmaKv>();
+            wait_vm_lgkm0<3 * C::kDmaKv>();
         } else {
             wait_vm_lgkm0<0>();
         }
@@ -844,9 +846,9 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                         acc[u][kb] = mfma_32x32x16t<kBf16>(xt[u][ks], bp[ks][kb], acc[u][kb]);
         };
         auto prologue = [&](const FA3_LDS char* __restrict__ s0) {
-            read_xt(s0, xa);
-            wait_vm_lgkm0<2 * C::kDmaKv>();
+            wait_vm_lgkm0<2 * C::kDmaKv>();  // the first tile has landed
             barrier();
+            read_xt(s0, xa);
         };
         auto step = [&](FA3_LDS char* __restrict__ ld, const FA3_LDS char* __restrict__ s1,
                         const FA3_LDS char* __restrict__ prd, const f16x8 (&xcur)[kPpw][4],
@@ -968,11 +970,11 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         load_tile_async(ds0, a.q + q0, q_off, w);
         load_tile_async(ds0 + C::kTileBytes, a.dout + q0, q_off, w);
         load_rows_async<kRows>(st_ld + 2 * C::kTileBytes, a, row0, w, lane);
-        if (loads) {
+        if (loads) {  // as in dkv_role: Q, dO and the rows first
             issue(st_ld);
             issue(st_1);
             issue(st_2);
-            wait_vm_lgkm0<2 * C::kDmaQ>();
+            wait_vm_lgkm0<3 * C::kDmaQ>();
         } else {
             wait_vm_lgkm0<0>();
         }
@@ -1105,9 +1107,9 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
                 for (int r = 0; r < kRb; ++r) acc[r] = mfma_32x32x16t<kBf16>(xt[ks], bd[ks][r], acc[r]);
         };
         auto prologue = [&](const FA3_LDS char* __restrict__ s0) {
-            read_xt(s0, xa);
             wait_vm_lgkm0<2 * C::kDmaQ>();
             barrier();
+            read_xt(s0, xa);
         };
         auto step = [&](FA3_LDS char* __restrict__ ld, const FA3_LDS char* __restrict__ s1,
                         const FA3_LDS char* __restrict__ prd, const f16x8 (&xcur)[4],
