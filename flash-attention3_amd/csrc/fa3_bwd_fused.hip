@@ -131,14 +131,6 @@ struct Cfg {
     // direct-to-LDS loads per loading wave and stage: dKV Q, dO, rows; dQ K, V
     static constexpr int kDmaKv = 2 * kNld + 1;
     static constexpr int kDmaQ = 2 * kNld;
-    // phase-2 split: the dKV role has 2 * kDB (matrix, D-slice) pairs, the dQ
-    // role kDB D-slices; the 8 waves cover them with kSplitKv / kSplitQ waves
-    // each, splitting the 4 contraction steps of a tile between them.
-    static constexpr int kPairsKv = 2 * kDB;
-    static constexpr int kSplitKv = kWaves / kPairsKv;
-    static constexpr int kStepsKv = 4 / kSplitKv;
-    static constexpr int kSplitQ = kWaves / kDB;
-    static constexpr int kStepsQ = 4 / kSplitQ;
     static constexpr int kPdsBytes = 64 * 64 * 2;           // one [64][64] fp16 tile
     static constexpr int kPdsOff = kStages * kStageBytes;   // P / dS double buffer
     static constexpr int kFlagOff = kPdsOff + 2 * 2 * kPdsBytes;  // split-plan flag word
