@@ -114,6 +114,35 @@ def test_split_plan_reused_workspace(hq, s, d):
         check(res, g)
 
 
+@pytest.mark.parametrize("hq,s,d", [(4, 2048, 128), (2, 1024, 64)])
+def test_split_plan_back_to_back_calls(hq, s, d):
+    """Many v2 calls queued on the null stream without synchronisation (one
+    workspace, as a training loop would): each call's preprocess clears the
+    split counters the previous call's main kernel used, so stream order must
+    hold; the last result is bitwise the synchronised one."""
+    log(f"[case] back-to-back calls Hq{hq} S{s} D{d}")
+    lib = F.load()
+    g = O.golden(1, hq, hq, s, d, True)
+    ref = run_v2(g, torch)
+    check(ref, g)
+    q, k, v, do, out = (dev(g[n], torch) for n in ("q", "k", "v", "dout", "out"))
+    lse = dev(g["lse"], torch)
+    p = F.make_params(lib, batch=1, seqlen=s, heads_q=hq, head_dim=d, causal=True,
+                      softmax_scale=g["scale"])
+    nbytes = lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    c = lambda x: ctypes.c_void_p(x.data_ptr())  # noqa: E731
+    for _ in range(200):
+        st = lib.shaobo_fa3_bwd_v2(c(do), c(q), c(k), c(v), c(out), c(lse), c(dq), c(dk), c(dv),
+                                   None, ctypes.byref(p))
+        assert st == F.SUCCESS
+    torch.cuda.synchronize()
+    for n, t in (("dq", dq), ("dk", dk), ("dv", dv)):
+        np.testing.assert_array_equal(t.float().cpu().numpy(), ref[n])
+
+
 def test_default_scale_and_internal_delta():
     """softmax_scale_is_set = 0 -> 1/sqrt(D); softmax_d = NULL keeps delta internal."""
     log("[case] default scale, softmax_d NULL")
