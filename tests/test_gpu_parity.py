@@ -143,6 +143,45 @@ def test_split_plan_back_to_back_calls(hq, s, d):
         np.testing.assert_array_equal(t.float().cpu().numpy(), ref[n])
 
 
+def test_concurrent_calls_on_two_streams():
+    """Two different problems launched on two streams through the stream entry
+    (shaobo_fa3_bwd_v2_on_stream), each with its own workspace: the library
+    keeps no state between calls, so both match their oracles."""
+    log("[case] concurrent calls on two streams")
+    lib = F.load()
+    fn = lib.shaobo_fa3_bwd_v2_on_stream
+    fn.argtypes = [ctypes.c_void_p] * 10 + [ctypes.POINTER(F.Params), ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    c = lambda x: ctypes.c_void_p(x.data_ptr())  # noqa: E731
+    gs = [O.golden(1, 4, 4, 2048, 128, True), O.golden(2, 4, 2, 512, 64, False, seed_offset=7)]
+    keep, outs = [], []
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for g, stream in zip(gs, streams):
+        B, Hq, S, D = g["q"].shape
+        Hkv = g["k"].shape[1]
+        q, k, v, do, out = (dev(g[n], torch) for n in ("q", "k", "v", "dout", "out"))
+        lse = dev(g["lse"], torch)
+        p = F.make_params(lib, batch=B, seqlen=S, heads_q=Hq, heads_kv=Hkv, head_dim=D,
+                          causal=g["causal"], softmax_scale=g["scale"])
+        nbytes = lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        delta = torch.empty((B, Hq, S), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()  # inputs written before either stream starts
+        st = fn(c(do), c(q), c(k), c(v), c(out), c(lse), c(dq), c(dk), c(dv), c(delta),
+                ctypes.byref(p), ctypes.c_void_p(stream.cuda_stream))
+        assert st == F.SUCCESS
+        keep.append((q, k, v, do, out, lse, ws, p))
+        outs.append((dq, dk, dv, delta))
+    torch.cuda.synchronize()
+    for g, (dq, dk, dv, delta) in zip(gs, outs):
+        res = {"dq": dq.float().cpu().numpy(), "dk": dk.float().cpu().numpy(),
+               "dv": dv.float().cpu().numpy(), "delta": delta.cpu().numpy()}
+        check(res, g)
+
+
 def test_default_scale_and_internal_delta():
     """softmax_scale_is_set = 0 -> 1/sqrt(D); softmax_d = NULL keeps delta internal."""
     log("[case] default scale, softmax_d NULL")
