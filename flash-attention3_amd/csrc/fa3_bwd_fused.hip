@@ -831,6 +831,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                 for (int kb = 0; kb < 2; ++kb)
                     bp[ks][kb] = lds_read_b128(m, dst_off(32 * kb + l32, 2 * ks + h));
             __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+            set_prio<0>();  // raised for the step's LDS reads (see step)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -852,7 +853,10 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
             __builtin_amdgcn_sched_barrier(0);
             // next tile's operands first: the LDS reads run while the score
             // waves' (higher priority) MFMAs hold the matrix unit, and this
-            // wave's MFMAs overlap their softmax instead
+            // wave's MFMAs overlap their softmax instead.  The reads go out at
+            // priority 2 (below the score waves' MFMA phase, above their
+            // softmax), so they are not held back behind the softmax (P3 -1 %).
+            set_prio<2>();
             read_xt(s1, xnext);
             grad(xcur, prd);
             __builtin_amdgcn_sched_barrier(0);
@@ -1095,6 +1099,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
                 for (int r = 0; r < kRb; ++r)
                     bd[ks][r] = lds_read_b128(ds, dst_off(32 * (rb0 + r) + l32, 2 * ks + h));
             __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+            set_prio<0>();  // as in dkv_role
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -1111,9 +1116,8 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
             top();
             issue(ld);
             __builtin_amdgcn_sched_barrier(0);
-            // next tile's operands first: the LDS reads run while the score
-            // waves' (higher priority) MFMAs hold the matrix unit, and this
-            // wave's MFMAs overlap their softmax instead
+            // as in dkv_role
+            set_prio<2>();
             read_xt(s1, xnext);
             grad(xcur, prd);
             __builtin_amdgcn_sched_barrier(0);
