@@ -1,12 +1,13 @@
 """Benchmark of the FA3 backward (shaobo_fa3_bwd_v2) on one MI355X.
 
-A step is one full backward (delta preprocess kernel -> main kernel) through
-the C ABI over resident fp16 inputs at the headline shape
-B=1, H=4, S=2048, D=128, causal.  Prints one JSON
-line: TFLOP/s from FLOPs = 10*B*H*S^2*D*0.5, ms per backward, % of fp16 dense
-MFMA peak, the main kernel's roofline (HIP events recorded by the library at
-its stage boundaries on the null stream, where it launches), and the CPU
-oracle timed on the host as the reported CPU baseline.
+A step is one full backward through the C ABI over resident fp16 inputs at
+the headline shape B=1, H=4, S=2048, D=128, causal (BASELINE.json
+configs[2]).  v2 is one kernel launch (the main kernel forms delta and lse2
+itself), so the step's HIP events, recorded on the null stream where the
+library launches, time the main kernel back to back.  Prints one JSON line:
+TFLOP/s from FLOPs = 10*B*H*S^2*D*0.5, ms per backward, % of fp16 dense MFMA
+peak, the main kernel's roofline, and the CPU oracle timed on the host as the
+reported CPU baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config P3]
 """
@@ -24,7 +25,6 @@ sys.path.insert(0, os.path.join(ROOT, "flash-attention3_amd"))
 METRIC = "FA bwd TFLOPS + % fp16 MFMA peak, B1 H4 S2048 D128 causal fp16; ms/bwd"
 FP16_PEAK_TFLOPS = 2516.6   # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
 HBM_PEAK_GBS = 8000.0
-STAGE_TAG = 0x53544745      # reserved_i32[15]: record stage events (library hook)
 
 CONFIGS = {
     # name: (B, Hq, Hkv, S, D, causal)
@@ -94,8 +94,8 @@ class Hip:
 def load_traffic(config):
     """HBM bytes per launch of the main kernel, measured with rocprofv3
     FETCH_SIZE / WRITE_SIZE and scaled by a copy kernel of known size
-    (profiles/traffic_bwd_fused_kernel.json, written from those runs)."""
-    path = os.path.join(ROOT, "profiles", "traffic_bwd_fused_kernel.json")
+    (profiles/traffic_bwd_main_kernel.json, written from those runs)."""
+    path = os.path.join(ROOT, "profiles", "traffic_bwd_main_kernel.json")
     try:
         with open(path) as fh:
             entry = json.load(fh).get(config)
@@ -141,8 +141,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=None,
-                    help="untimed warm-up steps (default: at least 20, and enough for "
-                         "0.2 s of GPU work, which brings the clocks to their steady state)")
+                    help="untimed warm-up steps (default 20); warm-up also lasts at least "
+                         "0.3 s of GPU work, which brings the clocks to their steady state")
     ap.add_argument("--config", default="P3", choices=sorted(CONFIGS))
     ap.add_argument("--deterministic", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
@@ -181,20 +181,20 @@ def main():
         if st != F.SUCCESS:
             raise RuntimeError("shaobo_fa3_bwd_v2: " + F.status_name(st))
 
-    if args.warmup is not None:
-        for _ in range(args.warmup):
+    # Warm-up: at least `warmup` steps (default 20) and at least 0.3 s of
+    # GPU work, in batches of 20 -- the GPU's clocks ramp up over tens of
+    # milliseconds of sustained work, and a handful of steps measures the
+    # ramp instead of the kernel.
+    want = 20 if args.warmup is None else args.warmup
+    done = 0
+    t_w = time.perf_counter()
+    while done < want or time.perf_counter() - t_w < 0.3:
+        for _ in range(20):
             step()
+        done += 20
         torch.cuda.synchronize()
-    else:
-        # The GPU's clocks ramp up over tens of milliseconds of sustained work:
-        # warm up for at least 0.2 s (and 20 steps), in batches of 20.
-        args.warmup = 0
-        t_w = time.perf_counter()
-        while args.warmup < 20 or time.perf_counter() - t_w < 0.2:
-            for _ in range(20):
-                step()
-            args.warmup += 20
-            torch.cuda.synchronize()
+    warm_s = time.perf_counter() - t_w
+    args.warmup = want
 
     # ---- timed region: exactly `steps` backward lifecycles ----
     e0, e1 = hip.event(), hip.event()
@@ -210,23 +210,8 @@ def main():
     f = flops(B, Hq, S, D, causal)
     tflops = f / (ms * 1e-3) / 1e12
 
-    # ---- per-kernel durations from the library's stage events (null stream) ----
-    evs = [hip.event() for _ in range(4)]
-    p.reserved_i32[15] = STAGE_TAG
-    for i, e in enumerate(evs):
-        p.reserved_ptr[4 + i] = e.value
-    stage = [0.0, 0.0]
-    for _ in range(args.steps):
-        step()
-        hip.sync()
-        for i in range(2):
-            stage[i] += hip.elapsed_ms(evs[i], evs[i + 1])
-    p.reserved_i32[15] = 0
-    stage = [s / args.steps for s in stage]
-    pre_ms, main_ms = stage
-    rows = B * Hq * S
-    # preprocess algorithmic bytes: read O, dO (fp16) and LSE; write delta, lse2
-    pre_bytes = rows * D * 2 * 2 + rows * 4 * 3
+    # v2 is one launch per step: the step time is the main kernel's, back to back
+    main_ms = ms
     main_tflops = f / (main_ms * 1e-3) / 1e12
     traffic = load_traffic(args.config)
     result = {
@@ -249,16 +234,14 @@ def main():
                    "flops_per_bwd": f},
         "pct_fp16_peak": round(100.0 * tflops / FP16_PEAK_TFLOPS, 3),
         "wall_s_timed": round(wall, 4),
-        "kernels_ms": {"preprocess_kernel": round(pre_ms, 5), "bwd_fused_kernel": round(main_ms, 5)},
-        "roofline": {"kernel": "bwd_fused_kernel", "bound": "mfma",
+        "warmup_steps_run": done,
+        "warmup_s": round(warm_s, 3),
+        "kernels_ms": {"bwd_main_kernel": round(main_ms, 5)},
+        "roofline": {"kernel": "bwd_main_kernel", "bound": "mfma",
                      "achieved": round(main_tflops, 3),
                      "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(main_tflops / FP16_PEAK_TFLOPS, 5),
                      "traffic": traffic},
-        "preprocess_roofline": {"kernel": "preprocess_kernel", "bound": "hbm",
-                                "achieved": round(pre_bytes / (pre_ms * 1e-3) / 1e9, 1),
-                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                "frac": round(pre_bytes / (pre_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
     }
     if args.calib_copy_mb > 0:
         # plain copy kernel of known size, for scaling rocprofv3 FETCH/WRITE_SIZE

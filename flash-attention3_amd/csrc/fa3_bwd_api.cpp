@@ -122,15 +122,30 @@ fa3::BwdProblem problem_of(const ShaoboFa3Params* p) {
 }
 
 // sync_after_launch: the whole device for the null stream (reference
-// behaviour), the caller's stream otherwise.
-int finish(hipError_t err, const ShaoboFa3Params* p, hipStream_t stream = nullptr) {
+// behaviour), the caller's stream otherwise.  When the launch used the split
+// plan, the synchronised call also reads the workspace's error word: a split
+// wait that gave up wrote the launch's epoch there, and the call reports a
+// HIP error instead of returning wrong gradients as success.
+int finish(hipError_t err, const ShaoboFa3Params* p, hipStream_t stream = nullptr,
+           const void* err_word = nullptr, unsigned long long epoch = 0) {
     if (err != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
     if (p->sync_after_launch) {
         const hipError_t e = stream == nullptr ? hipDeviceSynchronize() : hipStreamSynchronize(stream);
         if (e != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
+        if (err_word != nullptr) {
+            unsigned long long word = 0;
+            if (hipMemcpy(&word, err_word, sizeof(word), hipMemcpyDeviceToHost) != hipSuccess ||
+                word == epoch) {
+                return SHAOBO_FA3_STATUS_HIP_ERROR;
+            }
+        }
     }
     return SHAOBO_FA3_STATUS_SUCCESS;
 }
+
+// Row statistics formed inside the main kernel (natural-log LSE input), or by
+// a preprocess pass into workspace arrays (raw max / sum, packed sidecar).
+bool rows_inline(bool aux_is_lse, bool packed) { return aux_is_lse && !packed; }
 
 // Shared body of v2 and the legacy entry.
 int run_backward(const void* dout, const void* q, const void* k, const void* v, const void* out,
@@ -145,7 +160,7 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
         return SHAOBO_FA3_STATUS_INVALID_VALUE;
     }
     const fa3::BwdProblem pr = problem_of(params);
-    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr);
+    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr, rows_inline(aux_is_lse, false));
     if (!plan.ok || params->workspace == nullptr || params->workspace_bytes < plan.total) {
         return SHAOBO_FA3_STATUS_INVALID_VALUE;
     }
@@ -163,17 +178,17 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
     t.dv = dv;
     t.delta = static_cast<float*>(softmax_d);
     t.stream = stream;
-    if (params->reserved_i32[15] == fa3::kStageEventTag) {
-        for (int i = 0; i < 4; ++i) {
-            t.stage_events[i] = static_cast<hipEvent_t>(params->reserved_ptr[4 + i]);
-        }
-    }
-    return finish(fa3::launch_backward(pr, t, params->workspace), params, stream);
+    unsigned long long epoch = 0;
+    const hipError_t err = fa3::launch_backward(pr, t, params->workspace, &epoch);
+    const char* ws = static_cast<const char*>(params->workspace);
+    return finish(err, params, stream, plan.bal_m > 0 ? ws + plan.err_off : nullptr, epoch);
 }
 
-size_t workspace_bytes_of(const ShaoboFa3Params* params) {
+// v2 takes the natural-log LSE; the legacy entry follows softmax_aux_mode.
+size_t workspace_bytes_of(const ShaoboFa3Params* params, bool aux_is_lse) {
     if (validate(params) != SHAOBO_FA3_STATUS_SUCCESS) return 0;
-    const fa3::WorkspacePlan plan = fa3::plan_workspace(problem_of(params));
+    const fa3::WorkspacePlan plan =
+        fa3::plan_workspace(problem_of(params), rows_inline(aux_is_lse, false));
     return plan.ok ? plan.total : 0;
 }
 
@@ -222,8 +237,9 @@ fa3::BwdProblem component_problem(const ShaoboFa3Params* p, bool out_f32) {
     return pr;
 }
 
+// fused5: rows from the packed sidecar
 size_t component_workspace(const fa3::BwdProblem& pr) {
-    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr);
+    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr, rows_inline(true, true));
     return plan.ok ? plan.total : 0;
 }
 
@@ -262,7 +278,7 @@ int shaobo_fa3_bwd_get_capabilities(ShaoboFa3BwdCapabilities* caps) {
 int shaobo_fa3_bwd_v2_validate(const ShaoboFa3Params* params) { return validate(params); }
 
 size_t shaobo_fa3_bwd_v2_workspace_bytes(const ShaoboFa3Params* params) {
-    return workspace_bytes_of(params);
+    return workspace_bytes_of(params, true);
 }
 
 int shaobo_fa3_bwd_v2(const void* dout, const void* q, const void* k, const void* v,
@@ -280,6 +296,8 @@ int shaobo_fa3_bwd_v2_on_stream(const void* dout, const void* q, const void* k, 
                         params, static_cast<hipStream_t>(stream));
 }
 
+void shaobo_fa3_ext_set_split_spin_limit(int polls) { fa3::set_split_spin_limit(polls); }
+
 const char* shaobo_fa3_status_string(int status) {
     switch (status) {
         case SHAOBO_FA3_STATUS_SUCCESS: return "success";
@@ -292,7 +310,8 @@ const char* shaobo_fa3_status_string(int status) {
 }
 
 size_t shaobo_fa3_bwd_workspace_bytes(const ShaoboFa3Params* params) {
-    return workspace_bytes_of(params);
+    if (params == nullptr) return 0;
+    return workspace_bytes_of(params, params->softmax_aux_mode != SHAOBO_FA3_SOFTMAX_AUX_SMAX_SSUM);
 }
 
 int shaobo_fa3_bwd(const void* dout, const void* q, const void* k, const void* v,
@@ -369,11 +388,14 @@ int shaobo_fa3_bwd_fused5(const void* dout, const void* q, const void* k, const 
     t.dk = dk;
     t.dv = dv;
     const fa3::BwdProblem pr = component_problem(params, false);
-    const size_t need = component_workspace(pr);
-    if (need == 0 || params->workspace == nullptr || params->workspace_bytes < need) {
+    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr, rows_inline(true, true));
+    if (!plan.ok || params->workspace == nullptr || params->workspace_bytes < plan.total) {
         return SHAOBO_FA3_STATUS_INVALID_VALUE;
     }
-    return finish(fa3::launch_backward(pr, t, params->workspace), params);
+    unsigned long long epoch = 0;
+    const hipError_t err = fa3::launch_backward(pr, t, params->workspace, &epoch);
+    const char* ws = static_cast<const char*>(params->workspace);
+    return finish(err, params, nullptr, plan.bal_m > 0 ? ws + plan.err_off : nullptr, epoch);
 }
 
 size_t shaobo_fa3_bwd_dkv_workspace_bytes(const ShaoboFa3Params* params) {

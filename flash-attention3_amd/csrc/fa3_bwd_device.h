@@ -34,28 +34,52 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.44269504088896340736f;
 
-// delta = sum_d fp32(dO[row, d]) * fp32(O[row, d]) of one query row whose
-// elements start at `elem` (fp16, or bf16 when kBf16): lane
-// `sub` of the row's D / 8 consecutive lanes takes one 16-byte chunk, then a
-// butterfly over those lanes (same order wherever it runs, so the preprocess
-// kernel and the fused preprocess give the same bits).
-template <int D, bool kBf16 = false>
-__device__ __forceinline__ float row_delta(const _Float16* dout, const _Float16* out, size_t elem,
-                                           int sub) {
-    const size_t base = elem + sub * 8;
-    const f16x8 a = *(const f16x8*)(dout + base);
-    const f16x8 b = *(const f16x8*)(out + base);
-    float acc = 0.f;
+// Partial dot product of 8 pairs of 16-bit values (fp16, or bf16 bits when
+// kBf16), accumulated in fp32 in a fixed order.
+template <bool kBf16>
+__device__ __forceinline__ float dot8(f16x8 a, f16x8 b, float acc) {
     if constexpr (kBf16) {
-        const bf16x8 ab = __builtin_bit_cast(bf16x8, a), bb = __builtin_bit_cast(bf16x8, b);
+        const bf16x8 x = __builtin_bit_cast(bf16x8, a), y = __builtin_bit_cast(bf16x8, b);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc += (float)ab[i] * (float)bb[i];
+        for (int i = 0; i < 8; ++i) acc = __builtin_fmaf((float)x[i], (float)y[i], acc);
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc += (float)a[i] * (float)b[i];
+        for (int i = 0; i < 4; ++i) {
+            const f16x2 x = {a[2 * i], a[2 * i + 1]}, y = {b[2 * i], b[2 * i + 1]};
+            acc = __builtin_amdgcn_fdot2(x, y, acc, false);
+        }
     }
+    return acc;
+}
+
+// 16-byte chunk of D that lane group g (of 4 per row) takes in k-step s of
+// a 16x16x32 MFMA operand read from a [rows][D] tile: the main kernel's
+// order (with the tile swizzle of tile_off<D> every ds_read_b128 is then
+// conflict-free; the order 4 s + g would put two lanes of a group on one
+// bank quad).  The delta sums below follow it, so that delta formed in the
+// main kernel and by the preprocess pass agree bit for bit.
+template <int D>
+__device__ __forceinline__ int p1_chunk(int s, int g) {
+    if constexpr (D == 128) return s + 4 * g;
+    else return s + 2 * (g >> 1) + 4 * (g & 1);
+}
+
+// delta = sum_d fp32(dO[row, d]) * fp32(O[row, d]) of one query row whose
+// elements start at `elem`, formed by 4 lanes (g = lane % 4 of 4 consecutive
+// lanes): lane g sums chunks p1_chunk(s, g), s = 0 .. D / 32 - 1, with dot8,
+// then the pairs (g0, g1), (g2, g3) are added and then the two halves --
+// the order in which the main kernel adds its lane groups.
+template <int D, bool kBf16 = false>
+__device__ __forceinline__ float row_delta4(const _Float16* dout, const _Float16* out, size_t elem,
+                                            int g) {
+    float acc = 0.f;
 #pragma unroll
-    for (int off = D / 16; off > 0; off >>= 1) acc += __shfl_xor(acc, off, D / 8);
+    for (int s = 0; s < D / 32; ++s) {
+        const size_t c = elem + (size_t)p1_chunk<D>(s, g) * 8;
+        acc = dot8<kBf16>(*(const f16x8*)(dout + c), *(const f16x8*)(out + c), acc);
+    }
+    acc += __shfl_xor(acc, 1, 4);
+    acc += __shfl_xor(acc, 2, 4);
     return acc;
 }
 

@@ -48,53 +48,61 @@ struct BwdTensors {
     // delta_in together with the raw max / sum pair in aux0 / aux1 (dQ).
     const float* packed_in = nullptr;
     const float* delta_in = nullptr;
-    // Optional profiling events recorded on the launch stream at the stage
-    // boundaries: before preprocess, before main, before dQ finalize, after.
-    hipEvent_t stage_events[4] = {nullptr, nullptr, nullptr, nullptr};
     // Stream of every launch (null: the legacy default stream, as in the
     // reference ABI; the stream entry points pass the caller's).
     hipStream_t stream = nullptr;
 };
 
-// params->reserved_i32[15] == kStageEventTag enables stage_events, taken
-// from params->reserved_ptr[4..7] (the reference leaves these unused on v2).
-constexpr int32_t kStageEventTag = 0x53544745;
-
-// Device workspace the v2 entry asks the caller for: fp32 lse2 rows, then
-// fp32 -delta rows; with the split plan (bal_m > 0) also the split jobs'
-// arrival counters and fp32 partial sums.  Regions are 256-B aligned.
+// Device workspace of the v2 / legacy / fused5 entries (regions 256-B
+// aligned):
+//   * the error word (one 64-bit word), set to the launch's epoch by a split
+//     wait that gives up;
+//   * lse2 and -delta rows, when the row statistics come from a preprocess
+//     pass instead of being formed in the main kernel (SMAX_SSUM aux mode,
+//     the packed sidecar of fused5);
+//   * split plan only (bal_m > 0): two 64-bit synchronisation words per
+//     split job of each role, and the fp32 partial sums of one piece per
+//     split job (dKV jobs, then dQ jobs).
 struct WorkspacePlan {
+    bool inline_rows = true;
+    size_t err_off = 0;
     size_t lse2_off = 0;
     size_t ndelta_off = 0;
     int bal_m = 0;          // > 0: split plan with M = bal_m
-    int n_counters = 0;
-    size_t cnt_off = 0;
+    int n_split = 0;        // split jobs per role
+    size_t sync_off = 0;
     size_t pkv_off = 0;     // dKV pieces' partial sums
     size_t pq_off = 0;      // dQ pieces' partial sums
     size_t total = 0;
-    bool ok = false;
+    bool ok = false;        // false: the sizes overflow size_t / the kernel's offsets
 };
 
-WorkspacePlan plan_workspace(const BwdProblem& p);
+// inline_rows: the main kernel forms lse2 = LSE log2 e and delta itself (LSE
+// aux mode, no packed sidecar given).
+WorkspacePlan plan_workspace(const BwdProblem& p, bool inline_rows);
 
-// Launches the backward on the null stream: delta preprocess, then the
-// main kernel.
-hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace);
+// Launches the backward on t.stream: with arrays-sourced rows, the delta /
+// lse2 preprocess first, then the main kernel.  *epoch receives the value
+// the launch's split waits compare with (and write into the error word when
+// they give up).
+hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace,
+                           unsigned long long* epoch);
 
 // Delta preprocess: delta into t.delta, lse2 and -delta into the given rows;
-// any of the three may be null; also clears n_counters ints at `counters`.
-// Alone, it is the component entry shaobo_fa3_bwd_dot_do_o.
+// any of the three may be null.  Alone, it is the component entry
+// shaobo_fa3_bwd_dot_do_o.
 hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
-                             float* ndelta, int* counters = nullptr, int n_counters = 0);
+                             float* ndelta);
 
-// lse2 and -delta rows from the packed sidecar t.packed_in; also clears the
-// counters.
-hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta,
-                           int* counters, int n_counters);
+// lse2 and -delta rows from the packed sidecar t.packed_in.
+hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta);
 
 // Workspace-free single-role components (causal, heads_q == heads_kv, fp32
 // outputs when p.out_f32): role 1 writes dK / dV from t.packed_in, role 2
 // writes dQ from aux0 (raw max), aux1 (sum) and t.delta_in.
 hipError_t launch_component(const BwdProblem& p, const BwdTensors& t, int role);
+
+// Polls a split wait makes before it gives up (test hook; default 1 << 24).
+void set_split_spin_limit(int polls);
 
 }  // namespace fa3

@@ -11,8 +11,9 @@
 // Optionally also writes the reference's packed sidecar
 // [row_max_log2, row_inv_sum, delta] (reference src/dot_do_o_kernel.cpp:49-61).
 //
-// HBM-bound: one 16-byte load of dO and of O per lane (D / 8 lanes per row),
-// an in-register dot, and a butterfly reduction over the row's lanes.
+// HBM-bound: 4 lanes per row, D / 32 16-byte loads of dO and of O per lane,
+// in-register dots and a 2-step butterfly over the row's lanes, in the order
+// the main kernel forms delta inline (row_delta4), so both agree bit for bit.
 #include "fa3_bwd_device.h"
 #include "fa3_bwd_internal.h"
 
@@ -26,12 +27,10 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const _Float16* __restrict__ dout, const _Float16* __restrict__ out,
     const float* __restrict__ aux0, const float* __restrict__ aux1,
     float* __restrict__ delta, float* __restrict__ lse2, float* __restrict__ ndelta,
-    float* __restrict__ packed, int* __restrict__ counters, int n_counters, int rows,
+    float* __restrict__ packed, int rows,
     float scale_log2, int heads_q, int seqlen, int q_rs, int q_hs) {
-    constexpr int kLanesPerRow = D / 8;
+    constexpr int kLanesPerRow = 4;
     constexpr int kRowsPerBlock = 256 / kLanesPerRow;
-    const int gid = blockIdx.x * 256 + threadIdx.x;
-    if (gid < n_counters) counters[gid] = 0;
     const int sub = threadIdx.x % kLanesPerRow;
     const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
     if (row >= rows) return;  // rows % kRowsPerBlock may be non-zero only at the tail
@@ -39,7 +38,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const int hs = heads_q * seqlen;
     const int b = row / hs, rem = row - b * hs, h = rem / seqlen, sq = rem - h * seqlen;
     const size_t elem = (size_t)b * hs * D + (size_t)h * q_hs + (size_t)sq * q_rs;
-    const float acc = row_delta<D, kBf16>(dout, out, elem, sub);
+    const float acc = row_delta4<D, kBf16>(dout, out, elem, sub);
 
     if (sub == 0) {
         float l2, max_log2, inv_sum;
@@ -65,19 +64,17 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
 }
 
 template <int D>
-hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta,
-                        int* counters, int n_counters) {
-    constexpr int kRowsPerBlock = 256 / (D / 8);
+hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta) {
+    constexpr int kRowsPerBlock = 256 / 4;
     const int rows = p.batch * p.heads_q * p.seqlen;
-    int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    if (blocks * 256 < n_counters) blocks = (n_counters + 255) / 256;
+    const int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
     const float scale_log2 = p.scale * kLog2e;
     const int q_rs = p.bshd ? p.heads_q * D : D;
     const int q_hs = p.bshd ? D : p.seqlen * D;
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), 0, t.stream, (const _Float16*)t.dout,
                            (const _Float16*)t.out, t.aux0, t.aux1, t.delta, lse2, ndelta,
-                           t.packed, counters, n_counters, rows, scale_log2, p.heads_q, p.seqlen,
+                           t.packed, rows, scale_log2, p.heads_q, p.seqlen,
                            q_rs, q_hs);
     };
     if (t.aux_is_lse) {
@@ -96,11 +93,8 @@ hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, f
 // log2 inv)), and -delta.
 __global__ __launch_bounds__(256) void rowstats_kernel(const float* __restrict__ packed,
                                                        float* __restrict__ lse2,
-                                                       float* __restrict__ ndelta,
-                                                       int* __restrict__ counters, int n_counters,
-                                                       int rows) {
+                                                       float* __restrict__ ndelta, int rows) {
     const int r = blockIdx.x * 256 + threadIdx.x;
-    if (r < n_counters) counters[r] = 0;
     if (r >= rows) return;
     lse2[r] = packed[(size_t)r * 3] - log2f(packed[(size_t)r * 3 + 1]);
     ndelta[r] = -packed[(size_t)r * 3 + 2];
@@ -108,19 +102,17 @@ __global__ __launch_bounds__(256) void rowstats_kernel(const float* __restrict__
 
 }  // namespace
 
-hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta,
-                           int* counters, int n_counters) {
+hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta) {
     const int rows = p.batch * p.heads_q * p.seqlen;
-    const int n = rows > n_counters ? rows : n_counters;
-    hipLaunchKernelGGL(rowstats_kernel, dim3((n + 255) / 256), dim3(256), 0, t.stream, t.packed_in,
-                       lse2, ndelta, counters, n_counters, rows);
+    hipLaunchKernelGGL(rowstats_kernel, dim3((rows + 255) / 256), dim3(256), 0, t.stream,
+                       t.packed_in, lse2, ndelta, rows);
     return hipGetLastError();
 }
 
 hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
-                             float* ndelta, int* counters, int n_counters) {
-    if (p.head_dim == 128) return launch_pre_d<128>(p, t, lse2, ndelta, counters, n_counters);
-    if (p.head_dim == 64) return launch_pre_d<64>(p, t, lse2, ndelta, counters, n_counters);
+                             float* ndelta) {
+    if (p.head_dim == 128) return launch_pre_d<128>(p, t, lse2, ndelta);
+    if (p.head_dim == 64) return launch_pre_d<64>(p, t, lse2, ndelta);
     return hipErrorInvalidValue;
 }
 

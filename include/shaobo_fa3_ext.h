@@ -33,6 +33,16 @@ int shaobo_fa3_bwd_v2_on_stream(const void* dout,
                                 const ShaoboFa3Params* params,
                                 void* stream);
 
+/* Test hook, no counterpart in the reference: the number of polls a split
+ * job's second piece makes while waiting for the first piece's partial sums
+ * before it gives up (default 1 << 24, each poll followed by a short sleep).
+ * A wait that gives up still finishes its workgroup normally, writes the
+ * launch's epoch into the workspace's error word and the synchronised call
+ * (sync_after_launch = 1) returns SHAOBO_FA3_STATUS_HIP_ERROR; 0 makes every
+ * split wait give up at once.  Process-wide; affects launches made after the
+ * call. */
+void shaobo_fa3_ext_set_split_spin_limit(int polls);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -168,27 +168,37 @@ def test_status_strings(lib):
     assert lib.shaobo_fa3_status_string(99).decode() == "unknown"
 
 
-def split_plan_bytes(batch, heads, seqlen, head_dim):
+ERR_REGION = 256  # the error word's 256-byte region opens every workspace
+
+
+def row_arrays_bytes(rows):
+    """lse2 and -delta rows (fp32, each region 256-byte aligned), present when
+    a preprocess pass forms the row statistics (SMAX_SSUM aux, fused5)."""
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    return 2 * align(rows * 4)
+
+
+def split_plan_bytes(batch, heads, seqlen, head_dim, arrays=False):
     """Workspace of the split plan (causal, one query head per KV head, at
-    most 512 jobs): lse2 rows, -delta rows, one int counter per split job
-    (B*H*QT/2 per role), then fp32 partial sums of both pieces of every split
-    job -- dK/dV: 4 waves x (D/64 pairs x 2 key blocks x 16) registers x 64
-    lanes, dQ: 4 waves x (D/64 x 16) x 64 -- each region 256-byte aligned."""
+    most 512 jobs): the error word's region, [lse2 and -delta rows], two
+    64-bit synchronisation words per split job of each role (B*H*QT/2 jobs per
+    role), then the fp32 partial sums of one piece per split job -- dK/dV:
+    4 waves x 2 matrices x D/64 tiles x 4 KiB, dQ: 4 waves x D/64 tiles x
+    4 KiB -- each region 256-byte aligned."""
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
     rows = batch * heads * seqlen
-    m = seqlen // 64 // 2
-    jobs = batch * heads * m
-    off = align(rows * 4) + align(rows * 4)
-    off = align(off + 2 * jobs * 4)
-    off = align(off + jobs * 2 * 4 * (head_dim // 64) * 2 * 16 * 64 * 4)
-    return align(off + jobs * 2 * 4 * (head_dim // 64) * 16 * 64 * 4)
+    jobs = batch * heads * (seqlen // 64 // 2)
+    off = ERR_REGION + (row_arrays_bytes(rows) if arrays else 0)
+    off = align(off + jobs * 4 * 8)
+    off = align(off + jobs * 4 * 2 * (head_dim // 64) * 4096)
+    return align(off + jobs * 4 * (head_dim // 64) * 4096)
 
 
 def test_workspace_sizes(lib):
-    """fp32 lse2 rows + fp32 -delta rows, each region 256-byte aligned, plus
-    the split plan's counters and partial sums where it applies; the
-    reference contract test requires a non-zero size for a supported shape
-    (fused_bwd_api_contract.cpp:60-63)."""
+    """v2 forms its row statistics in the kernel: its workspace is the error
+    word's region plus, where the split plan applies, its synchronisation
+    words and partial sums; the reference contract test requires a non-zero
+    size for a supported shape (fused_bwd_api_contract.cpp:60-63)."""
     def ws(**kw):
         p = F.make_params(lib, **kw)
         return lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
@@ -197,10 +207,34 @@ def test_workspace_sizes(lib):
     assert ws(batch=1, seqlen=2048, heads_q=4, deterministic=True) == split_plan_bytes(1, 4, 2048, 128)
     assert ws(batch=1, seqlen=512, heads_q=2, head_dim=64) == split_plan_bytes(1, 2, 512, 64)
     # no split: non-causal, GQA, too many jobs, or fewer than four query tiles
-    assert ws(batch=2, seqlen=8192, heads_q=16, head_dim=64, causal=False) == 2 * 2 * 16 * 8192 * 4
-    assert ws(batch=2, seqlen=4096, heads_q=32, heads_kv=8) == 2 * 2 * 32 * 4096 * 4
-    assert ws(batch=2, seqlen=4096, heads_q=4) == 2 * 2 * 4 * 4096 * 4
-    assert ws(batch=1, seqlen=128, heads_q=1) == 1024
+    assert ws(batch=2, seqlen=8192, heads_q=16, head_dim=64, causal=False) == ERR_REGION
+    assert ws(batch=2, seqlen=4096, heads_q=32, heads_kv=8) == ERR_REGION
+    assert ws(batch=2, seqlen=4096, heads_q=4) == ERR_REGION
+    assert ws(batch=1, seqlen=128, heads_q=1) == ERR_REGION
+
+
+def test_legacy_workspace_sizes(lib):
+    """The legacy entry with raw max / sum rows needs the preprocess pass's
+    lse2 / -delta arrays; with LSE it sizes like v2."""
+    def ws(mode, **kw):
+        p = F.make_params(lib, **kw)
+        p.softmax_aux_mode = mode
+        return lib.shaobo_fa3_bwd_workspace_bytes(ctypes.byref(p))
+    assert ws(F.AUX_LSE, batch=2, seqlen=4096, heads_q=4) == ERR_REGION
+    assert ws(F.AUX_SMAX_SSUM, batch=2, seqlen=4096, heads_q=4) == \
+        ERR_REGION + row_arrays_bytes(2 * 4 * 4096)
+    assert ws(F.AUX_SMAX_SSUM, batch=1, seqlen=2048, heads_q=4) == \
+        split_plan_bytes(1, 4, 2048, 128, arrays=True)
+
+
+def test_workspace_overflow_is_zero(lib):
+    """Absurd shapes whose workspace arithmetic would overflow size_t or the
+    kernel's 32-bit offsets report 0 bytes instead of a wrapped size."""
+    p = F.make_params(lib, batch=1 << 30, seqlen=1 << 30, heads_q=1 << 20)
+    p.softmax_aux_mode = F.AUX_SMAX_SSUM
+    assert lib.shaobo_fa3_bwd_workspace_bytes(ctypes.byref(p)) == 0
+    p = F.make_params(lib, batch=1 << 30, seqlen=1 << 30, heads_q=1 << 20)
+    assert lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p)) == 0
 
 
 def test_launch_error_paths_without_gpu(lib):
@@ -312,7 +346,8 @@ def component_params(lib, **kw):
 def test_component_workspace_sizes(lib):
     """dkv / dq need no workspace (as the reference's canonical paths,
     src/dkv_kernel.cpp:1289-1298, src/dq_kernel.cpp:1486-1495); fused5 needs
-    the v2 plan's rows (and split buffers), 0 for an unsupported shape."""
+    the v2 plan plus the lse2 / -delta arrays its sidecar is folded into, 0
+    for an unsupported shape."""
     for f in ("dkv", "dq"):
         fn = getattr(lib, f"shaobo_fa3_bwd_{f}_workspace_bytes")
         assert fn(ctypes.byref(component_params(lib))) == 0
@@ -320,9 +355,9 @@ def test_component_workspace_sizes(lib):
     ws5 = lib.shaobo_fa3_bwd_fused5_workspace_bytes
     assert ws5(None) == 0
     assert ws5(ctypes.byref(component_params(lib, seqlen=2048, heads_q=4))) == \
-        split_plan_bytes(1, 4, 2048, 128)
+        split_plan_bytes(1, 4, 2048, 128, arrays=True)
     p = component_params(lib, heads_q=4, heads_kv=2, causal=False)
-    assert ws5(ctypes.byref(p)) == 2 * 4 * 256 * 4
+    assert ws5(ctypes.byref(p)) == ERR_REGION + row_arrays_bytes(4 * 256)
     p = component_params(lib)
     p.seqlen_k = 512
     assert ws5(ctypes.byref(p)) == 0
