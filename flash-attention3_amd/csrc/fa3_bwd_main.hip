@@ -142,8 +142,9 @@ struct Cfg {
     // O rows (see dkv_role), at D 64 in an area of its own
     static constexpr int kXchgOff = kStages * kStageBytes;
     static constexpr int kXchgBytes = D == 128 ? 0 : 4 * 4096;
-    static constexpr int kFlagOff = kXchgOff + kXchgBytes;
-    static constexpr int kBytes = kFlagOff + 256;
+    static constexpr int kFlagOff = kXchgOff + kXchgBytes;   // split flag (one int)
+    static constexpr int kDeltaOff = kFlagOff + 256;         // delta partials, 256 B per wave
+    static constexpr int kBytes = kDeltaOff + 1024;
     static_assert(kStageBytes % 512 == 0, "bank-aligned stages");
     static_assert(kBytes <= 160 * 1024, "LDS budget");
     // epilogue reduction: 4 source waves x kTiles tiles x 4 KiB
@@ -156,6 +157,44 @@ template <int N>
 __device__ __forceinline__ void wait_vm_lgkm0() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+}
+
+// s_waitcnt vmcnt(N): all but the last N vector-memory operations have
+// completed (LDS accesses are not waited for).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// s_waitcnt lgkmcnt(N): all but this wave's last N LDS operations have
+// completed (LDS operations of a wave complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_lgkm() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x3F | (0x7 << 4) | (N << 8) | (0x3 << 14));
+}
+
+// Scheduling patterns for the current region (between sched_barriers):
+// kM MFMAs, each followed by a share of the region's VALU work (and, for
+// sched_interleave, kR memory instructions spread over the first MFMAs), so
+// that one wave keeps its matrix unit busy while its VALU runs the softmax.
+template <int kM, int kR>
+__device__ __forceinline__ void sched_interleave() {
+#pragma unroll
+    for (int i = 0; i < kM; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        if (i < kR) __builtin_amdgcn_sched_group_barrier(0x180 | 0x010, 1, 0);  // DS read / VMEM
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+    }
+}
+template <int kM>
+__device__ __forceinline__ void sched_interleave_valu() {
+#pragma unroll
+    for (int i = 0; i < kM; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+    }
 }
 
 // Workgroup barrier that the compiler may not move memory accesses across.
@@ -634,9 +673,17 @@ __device__ void dkv_role(const A& a, int bkv, int kt, int qa, int qb, int slot,
     const size_t step_e = (size_t)64 * a.q_rs;
     const size_t wrap_e = (size_t)a.q_hs - (size_t)(qb - qa - 1) * step_e;  // next head, tile qa
     const size_t wrap_row = (size_t)S - (size_t)(qb - qa - 1) * 64;
-    auto issue = [&](FA3_LDS char* st) {
-        load_tile_async<D>(st, a.q + ld_e, q_off, w);
-        load_tile_async<D>(st + T, a.dout + ld_e, q_off, w);
+    // part 0: Q, part 1: dO, part 2: O (kO) and the rows, then the cursor
+    // moves on; a step spreads its parts over its MFMAs
+    auto issue_part = [&](FA3_LDS char* st, int part) {
+        if (part == 0) {
+            load_tile_async<D>(st, a.q + ld_e, q_off, w);
+            return;
+        }
+        if (part == 1) {
+            load_tile_async<D>(st + T, a.dout + ld_e, q_off, w);
+            return;
+        }
         if constexpr (kO) load_tile_async<D>(st + 2 * T, a.out + ld_e, q_off, w);
         load_rows_async<kRows>(st + C::kRowsOff, a, ld_row, w, lane);
         if (--ld_left > 0) {
@@ -664,8 +711,8 @@ __device__ void dkv_role(const A& a, int bkv, int kt, int qa, int qb, int slot,
         const size_t k0 = kv_elem<D>(a, b, hkv, kbase);
         load_tile_async<D>(st2, a.k + k0, kv_off, w);
         load_tile_async<D>(st2 + T, a.v + k0, kv_off, w);
-        issue(st0);
-        issue(st1);
+        for (int part = 0; part < 3; ++part) issue_part(st0, part);
+        for (int part = 0; part < 3; ++part) issue_part(st1, part);
         wait_vm_lgkm0<2 * kDma>();
         barrier();
 #pragma unroll
@@ -676,6 +723,7 @@ __device__ void dkv_role(const A& a, int bkv, int kt, int qa, int qb, int slot,
                 kf[kb][s] = lds_read_b128(st2, off);
                 vf[kb][s] = lds_read_b128(st2 + T, off);
             }
+        wait_vm_lgkm0<63>();  // K / V read before stage 2 takes tile 2
     }
 
     // dV^T / dK^T partials over the pair's rows for D half ch: tile t = 2 n +
@@ -694,77 +742,105 @@ __device__ void dkv_role(const A& a, int bkv, int kt, int qa, int qb, int slot,
         else return smem + C::kXchgOff + x * 4096;
     };
 
-    // One tile: rows 16 w .. 16 w + 15 of the stage's Q / dO (/ O).  Phases
-    // are pinned in program order (sched_barrier) so that only one phase's
-    // operands are live beside K, V and the accumulators.
-    auto compute = [&](FA3_LDS char* __restrict__ st, auto masked_c) {
-        constexpr bool kMasked = decltype(masked_c)::value;
-        const FA3_LDS char* tq = st;
-        const FA3_LDS char* tdo = st + T;
-        const FA3_LDS char* rows = st + C::kRowsOff;
-        f16x8 aq[kKs], ad[kKs];
+    // The operands a wave reads for its own rows of a tile, prefetched during
+    // the previous step: the A operands of S and dP (rows 16 w + l16, D chunks
+    // p1_chunk(s, g4)) and the rows' statistics, turned into lse2 and -delta
+    // of rows 16 w + 4 g4 + i (the S / dP accumulator rows).  With inline rows,
+    // delta comes from O's matching chunks: the four lanes of a row add their
+    // parts through 256 bytes of LDS, which also moves the sums to the
+    // accumulators' layout, in the order (g0 + g1) + (g2 + g3).  The wave's rows were loaded by
+    // its own direct-to-LDS loads, so its own s_waitcnt is all they need.
+    f16x8 aq[kKs], ad[kKs], ao[kKs];
+    f32x4 l2, nd, rs0, rs1, rs2;
+    FA3_LDS char* dslot = smem + C::kDeltaOff + 256 * w;
+    // LDS reads issued by read_own, in order
+    constexpr int kOwnReads = (kO ? 3 : 2) * kKs + (kRows == kRowsPacked ? 3 : kRows == kRowsArrays ? 2 : 1);
+    auto read_own = [&](const FA3_LDS char* st) {
 #pragma unroll
         for (int s = 0; s < kKs; ++s) {
             const uint32_t off = tile_off<D>(16 * w + l16, p1_chunk<D>(s, g4));
-            aq[s] = lds_read_b128(tq, off);
-            ad[s] = lds_read_b128(tdo, off);
+            aq[s] = lds_read_b128(st, off);
+            ad[s] = lds_read_b128(st + T, off);
+            if constexpr (kO) ao[s] = lds_read_b128(st + 2 * T, off);
         }
-        // lse2 and delta of rows 16 w + 4 g4 + i
-        f32x4 l2, dl;
-        float drow = 0.f;  // kRowsInline: partial delta of row 16 w + l16
+        const FA3_LDS char* rows = st + C::kRowsOff;
         if constexpr (kRows == kRowsInline) {
-            const f32x4 lse = *(const FA3_LDS f32x4*)(rows + (16 * w + 4 * g4) * 4);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) l2[i] = lse[i] * kLog2e;
+            rs0 = *(const FA3_LDS f32x4*)(rows + (16 * w + 4 * g4) * 4);
         } else if constexpr (kRows == kRowsArrays) {
-            const FA3_LDS char* r = rows + 128 * w + 16 * g4;
-            l2 = *(const FA3_LDS f32x4*)r;
-            const f32x4 nd = *(const FA3_LDS f32x4*)(r + 64);
+            rs0 = *(const FA3_LDS f32x4*)(rows + 128 * w + 16 * g4);
+            rs1 = *(const FA3_LDS f32x4*)(rows + 128 * w + 16 * g4 + 64);
+        } else {
+            const FA3_LDS f32x4* r = (const FA3_LDS f32x4*)(rows + (16 * w + 4 * g4) * 12);
+            rs0 = r[0];
+            rs1 = r[1];
+            rs2 = r[2];
+        }
+    };
+    auto finish_own = [&]() {
+        if constexpr (kRows == kRowsInline) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) dl[i] = -nd[i];
+            for (int i = 0; i < 4; ++i) l2[i] = rs0[i] * kLog2e;
+            float drow = 0.f;
+#pragma unroll
+            for (int s = 0; s < kKs; ++s) drow = dot8<kBf16>(ad[s], ao[s], drow);
+            // partial of row l16 from lane group g4 -> slot [row][g4]; each
+            // lane then adds the four partials of rows 4 g4 + i
+            *(FA3_LDS float*)(dslot + 16 * l16 + 4 * g4) = drow;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const f32x4 q = *(const FA3_LDS f32x4*)(dslot + 16 * (4 * g4 + i));
+                nd[i] = (q[0] + q[1]) + (q[2] + q[3]);
+            }
+        } else if constexpr (kRows == kRowsArrays) {
+            l2 = rs0;
+            nd = rs1;
         } else {
             // [row][max_log2, inv_sum, delta]: exp2(x - m) * inv = exp2(x - (m - log2 inv))
-            const FA3_LDS f32x4* r = (const FA3_LDS f32x4*)(rows + (16 * w + 4 * g4) * 12);
-            const f32x4 r0 = r[0], r1 = r[1], r2 = r[2];
-            const float f[12] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1],
-                                 r1[2], r1[3], r2[0], r2[1], r2[2], r2[3]};
+            const float f[12] = {rs0[0], rs0[1], rs0[2], rs0[3], rs1[0], rs1[1],
+                                 rs1[2], rs1[3], rs2[0], rs2[1], rs2[2], rs2[3]};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 l2[i] = f[3 * i] - __log2f(f[3 * i + 1]);
-                dl[i] = f[3 * i + 2];
+                nd[i] = -f[3 * i + 2];
             }
         }
-        __builtin_amdgcn_sched_barrier(0);
-        // S (rows x keys 16 kb + l16) and dP
-        f32x4 sacc[4], pacc[4];
+    };
+    // nd holds +delta from the inline path until the step uses it; the sign is
+    // applied where the dP accumulators are seeded
+    constexpr float kNdSign = kRows == kRowsInline ? -1.f : 1.f;
+
+    // Phase A of one tile (rows 16 w .. 16 w + 15 of stage st), in groups
+    // whose MFMAs and VALU work the scheduler interleaves (sched_group_barrier):
+    //   G0: S and dP of key blocks 0, 1 (4 accumulator chains) beside the
+    //       transposed reads of the own-row gradient operands and the first
+    //       loads of tile j + 2;
+    //   G1: S and dP of key blocks 2, 3 beside the softmax of blocks 0, 1 and
+    //       their P / dS operands (key block mb 0, also written for the
+    //       partner);
+    //   G2: the own rows' dV^T / dK^T for mb 0 beside the softmax of blocks
+    //       2, 3 and the operands of mb 1;
+    //   G3: the own rows' dV^T / dK^T for mb 1, the rest of the loads.
+    auto phase_a = [&](FA3_LDS char* __restrict__ st, const FA3_LDS char* __restrict__ nxt1,
+                       FA3_LDS char* __restrict__ nxt2, bool prefetch, auto masked_c) {
+        constexpr bool kMasked = decltype(masked_c)::value;
+        const FA3_LDS char* tq = st;
+        const FA3_LDS char* tdo = st + T;
+        f32x4 sacc[4], pacc[4], p[4], ds[4];
+        f16x8 bo[kNh], bq[kNh], ap[2], as[2];
+        FA3_LDS char* mine = xchg(st, w);
+        const f32x4 ndl = nd * kNdSign;  // -delta of the accumulator rows
+        auto mfma_s_dp = [&](int kb0) {
 #pragma unroll
-        for (int s = 0; s < kKs; ++s)
+            for (int s = 0; s < kKs; ++s)
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                sacc[kb] = mfma16<kBf16>(aq[s], kf[kb][s], s == 0 ? f32x4{} : sacc[kb]);
-                pacc[kb] = mfma16<kBf16>(ad[s], vf[kb][s], s == 0 ? f32x4{} : pacc[kb]);
-            }
-        if constexpr (kRows == kRowsInline) {
-            // delta of the wave's rows from dO (still in registers) and O
-            const FA3_LDS char* to = st + 2 * T;
-#pragma unroll
-            for (int s = 0; s < kKs; ++s) {
-                const f16x8 ao = lds_read_b128(to, tile_off<D>(16 * w + l16, p1_chunk<D>(s, g4)));
-                drow = dot8<kBf16>(ad[s], ao, drow);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (kRows == kRowsInline) {
-            drow += __shfl_xor(drow, 16);
-            drow += __shfl_xor(drow, 32);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dl[i] = __shfl(drow, 4 * g4 + i);
-        }
-        // P = exp2(S c - lse2), dS = P (dP - delta); on the causal diagonal
-        // tile the keys after a row see nothing
-        f32x4 p[4], ds[4];
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+                for (int kb = kb0; kb < kb0 + 2; ++kb) {
+                    sacc[kb] = mfma16<kBf16>(aq[s], kf[kb][s], s == 0 ? f32x4{} : sacc[kb]);
+                    pacc[kb] = mfma16<kBf16>(ad[s], vf[kb][s], s == 0 ? ndl : pacc[kb]);
+                }
+        };
+        // P = exp2(S c - lse2), dS = P (dP - delta) of key block kb; on the
+        // causal diagonal tile the keys after a row see nothing
+        auto softmax = [&](int kb) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float x = fast_exp2(sacc[kb][i] * a.scale_log2 - l2[i]);
@@ -772,43 +848,65 @@ __device__ void dkv_role(const A& a, int bkv, int kt, int qa, int qb, int slot,
                     if (16 * kb + l16 > 16 * w + 4 * g4 + i) x = 0.f;
                 }
                 p[kb][i] = x;
-                ds[kb][i] = x * (pacc[kb][i] - dl[i]);
+                ds[kb][i] = x * pacc[kb][i];
             }
-        // operands of the gradient products: keys 32 mb + l % 32, rows 8 h + t
-        // of the wave's 16; the partner gets a copy through LDS
-        f16x8 ap[2], as[2];
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
+        };
+        // operands of the gradient products (keys 32 mb + l % 32, rows 8 h + t
+        // of the wave's 16) and their copy for the partner
+        auto operands = [&](int mb) {
             ap[mb] = c16_to_op32<kBf16>(p[2 * mb], p[2 * mb + 1]);
             as[mb] = c16_to_op32<kBf16>(ds[2 * mb], ds[2 * mb + 1]);
-        }
-        FA3_LDS char* mine = xchg(st, w);
-        if constexpr (kRows == kRowsInline && D == 128)
-            wait_vm_lgkm0<63>();  // this wave's O reads are done before it overwrites them
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
             lds_write_b128(mine, (0 * 2 + mb) * 1024 + lane * 16, ap[mb]);
             lds_write_b128(mine, (1 * 2 + mb) * 1024 + lane * 16, as[mb]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        // the wave's own rows first, while the partner finishes its operands
-        f16x8 bo[kNh], bq[kNh];
+        };
+        auto own_grad = [&](int mb) {
+#pragma unroll
+            for (int n = 0; n < kNh; ++n) {
+                accv[2 * n + mb] = mfma32<kBf16>(bo[n], ap[mb], accv[2 * n + mb]);
+                acck[2 * n + mb] = mfma32<kBf16>(bq[n], as[mb], acck[2 * n + mb]);
+            }
+        };
+        // G0
+        mfma_s_dp(0);
 #pragma unroll
         for (int n = 0; n < kNh; ++n) {
             bo[n] = tile_read_t<D>(tdo, ch * kNh + n, w, lane);
             bq[n] = tile_read_t<D>(tq, ch * kNh + n, w, lane);
         }
-#pragma unroll
-        for (int n = 0; n < kNh; ++n)
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-                accv[2 * n + mb] = mfma32<kBf16>(bo[n], ap[mb], accv[2 * n + mb]);
-                acck[2 * n + mb] = mfma32<kBf16>(bq[n], as[mb], acck[2 * n + mb]);
-            }
-        wait_vm_lgkm0<63>();
-        barrier();
-        // the partner's rows
-        const FA3_LDS char* theirs = xchg(st, pw);
+        issue_part(nxt2, 0);
+        sched_interleave<4 * kKs, 2 * kNh + C::kLd>();
+        __builtin_amdgcn_sched_barrier(0);
+        // G1
+        mfma_s_dp(2);
+        softmax(0);
+        softmax(1);
+        operands(0);
+        sched_interleave_valu<4 * kKs>();
+        __builtin_amdgcn_sched_barrier(0);
+        // G2
+        own_grad(0);
+        softmax(2);
+        softmax(3);
+        operands(1);
+        sched_interleave_valu<2 * kNh>();
+        __builtin_amdgcn_sched_barrier(0);
+        // G3 (and the prefetch of tile j + 1's own rows: its loads were issued
+        // a step ago; only tile j + 2's may still be in flight)
+        own_grad(1);
+        issue_part(nxt2, 1);
+        issue_part(nxt2, 2);
+        if (prefetch) {
+            wait_vm<kDma>();
+            read_own(nxt1);
+        }
+    };
+
+    // Phase B: the partner's rows (its P / dS operands and the matching
+    // transposed operands of this wave's D half); while they are read, the
+    // next tile's prefetched rows become lse2 / delta.
+    auto phase_b = [&](const FA3_LDS char* __restrict__ st, bool prefetch) {
+        const FA3_LDS char* theirs = xchg(const_cast<FA3_LDS char*>(st), pw);
+        f16x8 bo[kNh], bq[kNh], ap[2], as[2];
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
             ap[mb] = lds_read_b128(theirs, (0 * 2 + mb) * 1024 + lane * 16);
@@ -816,9 +914,10 @@ __device__ void dkv_role(const A& a, int bkv, int kt, int qa, int qb, int slot,
         }
 #pragma unroll
         for (int n = 0; n < kNh; ++n) {
-            bo[n] = tile_read_t<D>(tdo, ch * kNh + n, pw, lane);
-            bq[n] = tile_read_t<D>(tq, ch * kNh + n, pw, lane);
+            bo[n] = tile_read_t<D>(st + T, ch * kNh + n, pw, lane);
+            bq[n] = tile_read_t<D>(st, ch * kNh + n, pw, lane);
         }
+        if (prefetch) finish_own();
 #pragma unroll
         for (int n = 0; n < kNh; ++n)
 #pragma unroll
@@ -828,25 +927,30 @@ __device__ void dkv_role(const A& a, int bkv, int kt, int qa, int qb, int slot,
             }
     };
 
-    // ---- main loop: tile j lives in stage j % 3; tile j + 2 is issued into
-    // the stage of tile j - 1 once every wave has passed this step's barrier
-    int sm_qt = qa;  // query tile of the next compute
-    auto step = [&](FA3_LDS char* __restrict__ cur, FA3_LDS char* __restrict__ nxt2) {
-        wait_vm_lgkm0<kDma>();
-        barrier();
-        issue(nxt2);
-        const bool masked = kCausal && sm_qt == kt;
-        if (++sm_qt == qb) sm_qt = qa;
-        if (masked) compute(cur, std::true_type{});
-        else compute(cur, std::false_type{});
-    };
-    // (one step per iteration over rotating stage pointers: addresses are
-    // then formed from one runtime base instead of one set per stage)
+    // ---- main loop: tile j lives in stage j % 3; tile j + 2 goes into the
+    // stage of tile j - 1 once every wave has passed this step's first
+    // barrier.  One step per iteration over rotating stage pointers (addresses
+    // are then formed from one runtime base instead of one set per stage).
+    int sm_qt = qa;  // query tile of the next step
     FA3_LDS char* cur = st0;
     FA3_LDS char* nx1 = st1;
     FA3_LDS char* nx2 = st2;
+    wait_vm<kDma>();  // tile 0 (only tile 1 may be in flight)
+    read_own(cur);
+    finish_own();
     for (int j = 0; j < n_it; ++j) {
-        step(cur, nx2);
+        barrier();  // every wave is done with tile j - 1: its stage takes tile j + 2
+        const bool masked = kCausal && sm_qt == kt;
+        if (++sm_qt == qb) sm_qt = qa;
+        const bool prefetch = j + 1 < n_it;
+        if (masked) phase_a(cur, nx1, nx2, prefetch, std::true_type{});
+        else phase_a(cur, nx1, nx2, prefetch, std::false_type{});
+        // the exchange writes are done (the prefetch reads issued after them
+        // may still be in flight)
+        if (prefetch) wait_lgkm<kOwnReads>();
+        else wait_lgkm<0>();
+        barrier();
+        phase_b(cur, prefetch);
         FA3_LDS char* x = cur;
         cur = nx1;
         nx1 = nx2;
@@ -921,8 +1025,12 @@ __device__ void dq_role(const A& a, int bhq, int qt, int ka, int kb, int slot,
     int ld_kt = ka;
     size_t ld_e = (size_t)ka * 64 * a.kv_rs;
     const size_t step_e = (size_t)64 * a.kv_rs;
-    auto issue = [&](FA3_LDS char* st) {
-        load_tile_async<D>(st, kh + ld_e, kv_off, w);
+    // part 0: K, part 1: V, then the cursor moves on
+    auto issue_part = [&](FA3_LDS char* st, int part) {
+        if (part == 0) {
+            load_tile_async<D>(st, kh + ld_e, kv_off, w);
+            return;
+        }
         load_tile_async<D>(st + T, vh + ld_e, kv_off, w);
         if (ld_kt + 1 < kb) {
             ++ld_kt;
@@ -946,8 +1054,8 @@ __device__ void dq_role(const A& a, int bhq, int qt, int ka, int kb, int slot,
         load_tile_async<D>(st2 + T, a.dout + q0, q_off, w);
         if constexpr (kRows == kRowsInline) load_tile_async<D>(st2 + 2 * T, a.out + q0, q_off, w);
         load_rows_async<kRows>(st2 + C::kRowsOff, a, row0, w, lane);
-        issue(st0);
-        issue(st1);
+        for (int part = 0; part < 2; ++part) issue_part(st0, part);
+        for (int part = 0; part < 2; ++part) issue_part(st1, part);
         wait_vm_lgkm0<2 * kDma>();
         barrier();
         const FA3_LDS char* rows = st2 + C::kRowsOff;
@@ -993,37 +1101,46 @@ __device__ void dq_role(const A& a, int bhq, int qt, int ka, int kb, int slot,
 #pragma unroll
     for (int u = 0; u < C::kTiles; ++u) accq[u] = f32x16{};
 
-    // One key tile: keys 16 w .. 16 w + 15 of the stage's K / V.
-    auto compute = [&](const FA3_LDS char* __restrict__ st, auto masked_c) {
-        constexpr bool kMasked = decltype(masked_c)::value;
-        const FA3_LDS char* tk = st;
-        const FA3_LDS char* tv = st + T;
-        f16x8 ak[kKs], av[kKs];
+    // The A operands of S^T and dP^T for the wave's own keys of a tile (keys
+    // 16 w + l16, D chunks p1_chunk(s, g4)), prefetched one step ahead.  The
+    // wave reads only rows it loaded itself, so the loop has no barrier: each
+    // wave's s_waitcnt orders its own loads and reads.
+    f16x8 ak[kKs], av[kKs];
+    auto read_own = [&](const FA3_LDS char* st) {
 #pragma unroll
         for (int s = 0; s < kKs; ++s) {
             const uint32_t off = tile_off<D>(16 * w + l16, p1_chunk<D>(s, g4));
-            ak[s] = lds_read_b128(tk, off);
-            av[s] = lds_read_b128(tv, off);
+            ak[s] = lds_read_b128(st, off);
+            av[s] = lds_read_b128(st + T, off);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        // S^T (keys 16 w + 4 g4 + i x rows 16 rb + l16) and dP^T - delta
-        f32x4 sacc[4], pacc[4];
+    };
+
+    // One key tile (stage st), in groups whose MFMAs and VALU work the
+    // scheduler interleaves:
+    //   G0: S^T and dP^T of row blocks 0, 1 beside the K^T operand reads of
+    //       dQ^T and the first loads of tile j + 2;
+    //   G1: row blocks 2, 3 beside the softmax of blocks 0, 1 and their dS^T
+    //       operand (row block mb 0);
+    //   G2: dQ^T of mb 0 beside the softmax of blocks 2, 3;
+    //   G3: dQ^T of mb 1 and the rest of the loads.
+    auto compute = [&](const FA3_LDS char* __restrict__ st, const FA3_LDS char* __restrict__ nxt1,
+                       FA3_LDS char* __restrict__ nxt2, bool prefetch, auto masked_c) {
+        constexpr bool kMasked = decltype(masked_c)::value;
+        const FA3_LDS char* tk = st;
+        f32x4 sacc[4], pacc[4], ds[4];
+        f16x8 bk[kKs], as[2];
+        auto mfma_s_dp = [&](int rb0) {
 #pragma unroll
-        for (int s = 0; s < kKs; ++s)
+            for (int s = 0; s < kKs; ++s)
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
-                const float nd = -dlt[rb];
-                sacc[rb] = mfma16<kBf16>(ak[s], qf[rb][s], s == 0 ? f32x4{} : sacc[rb]);
-                pacc[rb] = mfma16<kBf16>(av[s], df[rb][s], s == 0 ? f32x4{nd, nd, nd, nd} : pacc[rb]);
-            }
-        __builtin_amdgcn_sched_barrier(0);
-        // K^T operands of dQ^T: D block nb, keys 16 w + 8 h + t
-        f16x8 bk[kKs];
-#pragma unroll
-        for (int nb = 0; nb < kKs; ++nb) bk[nb] = tile_read_t<D>(tk, nb, w, lane);
-        f32x4 ds[4];
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
+                for (int rb = rb0; rb < rb0 + 2; ++rb) {
+                    const float nd = -dlt[rb];
+                    sacc[rb] = mfma16<kBf16>(ak[s], qf[rb][s], s == 0 ? f32x4{} : sacc[rb]);
+                    pacc[rb] = mfma16<kBf16>(av[s], df[rb][s],
+                                             s == 0 ? f32x4{nd, nd, nd, nd} : pacc[rb]);
+                }
+        };
+        auto softmax = [&](int rb) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float x = fast_exp2(sacc[rb][i] * a.scale_log2 - l2[rb]) * pacc[rb][i];
@@ -1032,33 +1149,62 @@ __device__ void dq_role(const A& a, int bhq, int qt, int ka, int kb, int slot,
                 }
                 ds[rb][i] = x;
             }
-        // dS^T operands: rows 32 mb + l % 32, the wave's keys 8 h + t
-        f16x8 as[2];
+        };
+        // dQ^T += K^T dS^T for row block mb (dS^T operand: rows 32 mb + l % 32,
+        // the wave's keys 8 h + t)
+        auto grad = [&](int mb) {
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) as[mb] = c16_to_op32<kBf16>(ds[2 * mb], ds[2 * mb + 1]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int nb = 0; nb < kKs; ++nb)
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
+            for (int nb = 0; nb < kKs; ++nb)
                 accq[2 * nb + mb] = mfma32<kBf16>(bk[nb], as[mb], accq[2 * nb + mb]);
+        };
+        // G0
+        mfma_s_dp(0);
+        // K^T operands of dQ^T: D block nb, keys 16 w + 8 h + t
+#pragma unroll
+        for (int nb = 0; nb < kKs; ++nb) bk[nb] = tile_read_t<D>(tk, nb, w, lane);
+        issue_part(nxt2, 0);
+        sched_interleave<4 * kKs, kKs + C::kLd>();
+        __builtin_amdgcn_sched_barrier(0);
+        // G1
+        mfma_s_dp(2);
+        softmax(0);
+        softmax(1);
+        as[0] = c16_to_op32<kBf16>(ds[0], ds[1]);
+        sched_interleave_valu<4 * kKs>();
+        __builtin_amdgcn_sched_barrier(0);
+        // G2 (and the prefetch of tile j + 1's own keys: its loads were issued
+        // a step ago; only tile j + 2's first part may still be in flight)
+        grad(0);
+        softmax(2);
+        softmax(3);
+        as[1] = c16_to_op32<kBf16>(ds[2], ds[3]);
+        if (prefetch) {
+            wait_vm<C::kLd>();
+            read_own(nxt1);
+        }
+        sched_interleave_valu<kKs>();
+        __builtin_amdgcn_sched_barrier(0);
+        // G3
+        grad(1);
+        issue_part(nxt2, 1);
     };
 
     int cur_kt = ka;
-    auto step = [&](FA3_LDS char* __restrict__ cur, FA3_LDS char* __restrict__ nxt2) {
-        wait_vm_lgkm0<kDma>();
-        barrier();
-        issue(nxt2);
-        const bool masked = kCausal && cur_kt == qt;
-        ++cur_kt;
-        if (masked) compute(cur, std::true_type{});
-        else compute(cur, std::false_type{});
-    };
     FA3_LDS char* cur = st0;
     FA3_LDS char* nx1 = st1;
     FA3_LDS char* nx2 = st2;
+    // the prologue's barrier let every wave finish reading stage 2 (this
+    // tile's Q, dO, O) before any wave loads into it
+    wait_vm_lgkm0<63>();
+    barrier();
+    wait_vm<kDma>();  // key tile 0 (only tile 1 may be in flight)
+    read_own(cur);
     for (int j = 0; j < n_kt; ++j) {
-        step(cur, nx2);
+        const bool masked = kCausal && cur_kt == qt;
+        ++cur_kt;
+        const bool prefetch = j + 1 < n_kt;
+        if (masked) compute(cur, nx1, nx2, prefetch, std::true_type{});
+        else compute(cur, nx1, nx2, prefetch, std::false_type{});
         FA3_LDS char* x = cur;
         cur = nx1;
         nx1 = nx2;
@@ -1127,8 +1273,13 @@ __device__ __forceinline__ void job_of(const MainArgs& a, int& g, int& pos) {
 // The host picks the head lengths from a cost model of the steps, prologues
 // and epilogues so that the workgroups finish together (a length covering
 // the whole job leaves it unsplit).
+// Workgroups per CU: at head dim 64 two fit (registers <= 256 per wave, LDS
+// <= 80 KiB), so each SIMD runs two waves that hide each other's latencies.
+template <int D>
+constexpr int kBlocksPerCu = D == 64 ? 2 : 1;
+
 template <int D, bool kCausal, bool kBf16, int kRows>
-__global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(MainArgs a) {
+__global__ __launch_bounds__(kThreads, kBlocksPerCu<D>) void bwd_main_kernel(MainArgs a) {
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
     int g, pos;
