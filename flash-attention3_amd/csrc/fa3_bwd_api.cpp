@@ -143,10 +143,6 @@ int finish(hipError_t err, const ShaoboFa3Params* p, hipStream_t stream = nullpt
     return SHAOBO_FA3_STATUS_SUCCESS;
 }
 
-// Row statistics formed inside the main kernel (natural-log LSE input), or by
-// a preprocess pass into workspace arrays (raw max / sum, packed sidecar).
-bool rows_inline(bool aux_is_lse, bool packed) { return aux_is_lse && !packed; }
-
 // Shared body of v2 and the legacy entry.
 int run_backward(const void* dout, const void* q, const void* k, const void* v, const void* out,
                  const void* aux0, const void* aux1, bool aux_is_lse, void* dq, void* dk,
@@ -160,7 +156,7 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
         return SHAOBO_FA3_STATUS_INVALID_VALUE;
     }
     const fa3::BwdProblem pr = problem_of(params);
-    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr, rows_inline(aux_is_lse, false));
+    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr);
     if (!plan.ok || params->workspace == nullptr || params->workspace_bytes < plan.total) {
         return SHAOBO_FA3_STATUS_INVALID_VALUE;
     }
@@ -184,11 +180,10 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
     return finish(err, params, stream, plan.bal_m > 0 ? ws + plan.err_off : nullptr, epoch);
 }
 
-// v2 takes the natural-log LSE; the legacy entry follows softmax_aux_mode.
-size_t workspace_bytes_of(const ShaoboFa3Params* params, bool aux_is_lse) {
+// Workspace of v2 and of the legacy entry (the same whatever the aux mode).
+size_t workspace_bytes_of(const ShaoboFa3Params* params) {
     if (validate(params) != SHAOBO_FA3_STATUS_SUCCESS) return 0;
-    const fa3::WorkspacePlan plan =
-        fa3::plan_workspace(problem_of(params), rows_inline(aux_is_lse, false));
+    const fa3::WorkspacePlan plan = fa3::plan_workspace(problem_of(params));
     return plan.ok ? plan.total : 0;
 }
 
@@ -239,7 +234,7 @@ fa3::BwdProblem component_problem(const ShaoboFa3Params* p, bool out_f32) {
 
 // fused5: rows from the packed sidecar
 size_t component_workspace(const fa3::BwdProblem& pr) {
-    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr, rows_inline(true, true));
+    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr);
     return plan.ok ? plan.total : 0;
 }
 
@@ -278,7 +273,7 @@ int shaobo_fa3_bwd_get_capabilities(ShaoboFa3BwdCapabilities* caps) {
 int shaobo_fa3_bwd_v2_validate(const ShaoboFa3Params* params) { return validate(params); }
 
 size_t shaobo_fa3_bwd_v2_workspace_bytes(const ShaoboFa3Params* params) {
-    return workspace_bytes_of(params, true);
+    return workspace_bytes_of(params);
 }
 
 int shaobo_fa3_bwd_v2(const void* dout, const void* q, const void* k, const void* v,
@@ -311,7 +306,7 @@ const char* shaobo_fa3_status_string(int status) {
 
 size_t shaobo_fa3_bwd_workspace_bytes(const ShaoboFa3Params* params) {
     if (params == nullptr) return 0;
-    return workspace_bytes_of(params, params->softmax_aux_mode != SHAOBO_FA3_SOFTMAX_AUX_SMAX_SSUM);
+    return workspace_bytes_of(params);
 }
 
 int shaobo_fa3_bwd(const void* dout, const void* q, const void* k, const void* v,
@@ -388,7 +383,7 @@ int shaobo_fa3_bwd_fused5(const void* dout, const void* q, const void* k, const 
     t.dk = dk;
     t.dv = dv;
     const fa3::BwdProblem pr = component_problem(params, false);
-    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr, rows_inline(true, true));
+    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr);
     if (!plan.ok || params->workspace == nullptr || params->workspace_bytes < plan.total) {
         return SHAOBO_FA3_STATUS_INVALID_VALUE;
     }

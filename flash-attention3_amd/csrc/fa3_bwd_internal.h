@@ -57,14 +57,11 @@ struct BwdTensors {
 // aligned):
 //   * the error word (one 64-bit word), set to the launch's epoch by a split
 //     wait that gives up;
-//   * lse2 and -delta rows, when the row statistics come from a preprocess
-//     pass instead of being formed in the main kernel (SMAX_SSUM aux mode,
-//     the packed sidecar of fused5);
+//   * lse2 and -delta rows, written by the preprocess pass;
 //   * split plan only (bal_m > 0): two 64-bit synchronisation words per
 //     split job of each role, and the fp32 partial sums of one piece per
 //     split job (dKV jobs, then dQ jobs).
 struct WorkspacePlan {
-    bool inline_rows = true;
     size_t err_off = 0;
     size_t lse2_off = 0;
     size_t ndelta_off = 0;
@@ -77,12 +74,10 @@ struct WorkspacePlan {
     bool ok = false;        // false: the sizes overflow size_t / the kernel's offsets
 };
 
-// inline_rows: the main kernel forms lse2 = LSE log2 e and delta itself (LSE
-// aux mode, no packed sidecar given).
-WorkspacePlan plan_workspace(const BwdProblem& p, bool inline_rows);
+WorkspacePlan plan_workspace(const BwdProblem& p);
 
-// Launches the backward on t.stream: with arrays-sourced rows, the delta /
-// lse2 preprocess first, then the main kernel.  *epoch receives the value
+// Launches the backward on t.stream: the delta / lse2 preprocess (or the
+// packed sidecar's fold), then the main kernel.  *epoch receives the value
 // the launch's split waits compare with (and write into the error word when
 // they give up).
 hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace,

@@ -33,7 +33,7 @@ EXPORTS = (
     "shaobo_fa3_bwd_fused5_workspace_bytes", "shaobo_fa3_bwd_fused5",
     "shaobo_fa3_bwd_dkv_workspace_bytes", "shaobo_fa3_bwd_dkv",
     "shaobo_fa3_bwd_dq_workspace_bytes", "shaobo_fa3_bwd_dq",
-    "shaobo_fa3_bwd_v2_on_stream",
+    "shaobo_fa3_bwd_v2_on_stream", "shaobo_fa3_ext_set_split_spin_limit",
 )
 
 # Component path selectors (params.dkv_path / params.dq_path) of the canonical
@@ -143,6 +143,8 @@ def load(path=LIB_PATH):
         lib.shaobo_fa3_bwd_dkv.restype = ctypes.c_int
         lib.shaobo_fa3_bwd_dq.argtypes = [ctypes.c_void_p] * 10 + [ctypes.POINTER(Params)]
         lib.shaobo_fa3_bwd_dq.restype = ctypes.c_int
+        lib.shaobo_fa3_ext_set_split_spin_limit.argtypes = [ctypes.c_int]
+        lib.shaobo_fa3_ext_set_split_spin_limit.restype = None
         if path != LIB_PATH:
             return lib
         _LIB = lib

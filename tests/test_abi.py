@@ -172,15 +172,21 @@ ERR_REGION = 256  # the error word's 256-byte region opens every workspace
 
 
 def row_arrays_bytes(rows):
-    """lse2 and -delta rows (fp32, each region 256-byte aligned), present when
-    a preprocess pass forms the row statistics (SMAX_SSUM aux, fused5)."""
+    """lse2 and -delta rows (fp32, each region 256-byte aligned) that the
+    preprocess pass writes for the main kernel."""
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
     return 2 * align(rows * 4)
 
 
-def split_plan_bytes(batch, heads, seqlen, head_dim, arrays=False):
+def plain_bytes(batch, heads_q, seqlen):
+    """Workspace without the split plan: the error word's region and the row
+    arrays."""
+    return ERR_REGION + row_arrays_bytes(batch * heads_q * seqlen)
+
+
+def split_plan_bytes(batch, heads, seqlen, head_dim):
     """Workspace of the split plan (causal, one query head per KV head, at
-    most 512 jobs): the error word's region, [lse2 and -delta rows], two
+    most 512 jobs): the error word's region, lse2 and -delta rows, two
     64-bit synchronisation words per split job of each role (B*H*QT/2 jobs per
     role), then the fp32 partial sums of one piece per split job -- dK/dV:
     4 waves x 2 matrices x D/64 tiles x 4 KiB, dQ: 4 waves x D/64 tiles x
@@ -188,17 +194,17 @@ def split_plan_bytes(batch, heads, seqlen, head_dim, arrays=False):
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
     rows = batch * heads * seqlen
     jobs = batch * heads * (seqlen // 64 // 2)
-    off = ERR_REGION + (row_arrays_bytes(rows) if arrays else 0)
+    off = ERR_REGION + row_arrays_bytes(rows)
     off = align(off + jobs * 4 * 8)
     off = align(off + jobs * 4 * 2 * (head_dim // 64) * 4096)
     return align(off + jobs * 4 * (head_dim // 64) * 4096)
 
 
 def test_workspace_sizes(lib):
-    """v2 forms its row statistics in the kernel: its workspace is the error
-    word's region plus, where the split plan applies, its synchronisation
-    words and partial sums; the reference contract test requires a non-zero
-    size for a supported shape (fused_bwd_api_contract.cpp:60-63)."""
+    """v2's workspace: the error word's region, the row arrays and, where the
+    split plan applies, its synchronisation words and partial sums; the
+    reference contract test requires a non-zero size for a supported shape
+    (fused_bwd_api_contract.cpp:60-63)."""
     def ws(**kw):
         p = F.make_params(lib, **kw)
         return lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
@@ -207,24 +213,22 @@ def test_workspace_sizes(lib):
     assert ws(batch=1, seqlen=2048, heads_q=4, deterministic=True) == split_plan_bytes(1, 4, 2048, 128)
     assert ws(batch=1, seqlen=512, heads_q=2, head_dim=64) == split_plan_bytes(1, 2, 512, 64)
     # no split: non-causal, GQA, too many jobs, or fewer than four query tiles
-    assert ws(batch=2, seqlen=8192, heads_q=16, head_dim=64, causal=False) == ERR_REGION
-    assert ws(batch=2, seqlen=4096, heads_q=32, heads_kv=8) == ERR_REGION
-    assert ws(batch=2, seqlen=4096, heads_q=4) == ERR_REGION
-    assert ws(batch=1, seqlen=128, heads_q=1) == ERR_REGION
+    assert ws(batch=2, seqlen=8192, heads_q=16, head_dim=64, causal=False) == plain_bytes(2, 16, 8192)
+    assert ws(batch=2, seqlen=4096, heads_q=32, heads_kv=8) == plain_bytes(2, 32, 4096)
+    assert ws(batch=2, seqlen=4096, heads_q=4) == plain_bytes(2, 4, 4096)
+    assert ws(batch=1, seqlen=128, heads_q=1) == plain_bytes(1, 1, 128)
 
 
 def test_legacy_workspace_sizes(lib):
-    """The legacy entry with raw max / sum rows needs the preprocess pass's
-    lse2 / -delta arrays; with LSE it sizes like v2."""
+    """The legacy entry sizes like v2 in either aux mode."""
     def ws(mode, **kw):
         p = F.make_params(lib, **kw)
         p.softmax_aux_mode = mode
         return lib.shaobo_fa3_bwd_workspace_bytes(ctypes.byref(p))
-    assert ws(F.AUX_LSE, batch=2, seqlen=4096, heads_q=4) == ERR_REGION
-    assert ws(F.AUX_SMAX_SSUM, batch=2, seqlen=4096, heads_q=4) == \
-        ERR_REGION + row_arrays_bytes(2 * 4 * 4096)
-    assert ws(F.AUX_SMAX_SSUM, batch=1, seqlen=2048, heads_q=4) == \
-        split_plan_bytes(1, 4, 2048, 128, arrays=True)
+    assert ws(F.AUX_LSE, batch=2, seqlen=4096, heads_q=4) == plain_bytes(2, 4, 4096)
+    assert ws(F.AUX_SMAX_SSUM, batch=2, seqlen=4096, heads_q=4) == plain_bytes(2, 4, 4096)
+    assert ws(F.AUX_SMAX_SSUM, batch=1, seqlen=2048, heads_q=4) == split_plan_bytes(1, 4, 2048, 128)
+    assert ws(F.AUX_LSE, batch=1, seqlen=2048, heads_q=4) == split_plan_bytes(1, 4, 2048, 128)
 
 
 def test_workspace_overflow_is_zero(lib):
@@ -355,7 +359,7 @@ def test_component_workspace_sizes(lib):
     ws5 = lib.shaobo_fa3_bwd_fused5_workspace_bytes
     assert ws5(None) == 0
     assert ws5(ctypes.byref(component_params(lib, seqlen=2048, heads_q=4))) == \
-        split_plan_bytes(1, 4, 2048, 128, arrays=True)
+        split_plan_bytes(1, 4, 2048, 128)
     p = component_params(lib, heads_q=4, heads_kv=2, causal=False)
     assert ws5(ctypes.byref(p)) == ERR_REGION + row_arrays_bytes(4 * 256)
     p = component_params(lib)

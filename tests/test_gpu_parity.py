@@ -4,9 +4,8 @@ against the CPU oracle, through the C ABI, on the BASELINE configs.
 Bar (north star): max|err|/max|ref| <= 1e-2 for dQ/dK/dV, delta within 1e-4
 relative; the reference's own gates (src/full_bwd_correctness.cpp:471-500)
 are asserted too on its deterministic pattern inputs, for which its absolute
-bounds were designed.  Large configs compare whole (batch, kv-head) groups
-computed by the oracle, and check every head through size-independent
-properties.
+bounds were designed.  The full-size configs compare every (batch, kv-head)
+group with the oracle.
 """
 import ctypes
 
@@ -97,9 +96,10 @@ def test_deterministic_mode_is_bitwise_repeatable(hq, hkv, s, d):
 @pytest.mark.parametrize("hq,s,d", [(2, 1024, 128), (4, 2048, 128), (2, 512, 64)])
 def test_split_plan_reused_workspace(hq, s, d):
     """Split plan, one workspace kept across calls on different inputs: the
-    partial sums and arrival counters of one call must never leak into the
-    next (counters are cleared per call; partial sums are read only after the
-    other piece of the same call has written them)."""
+    partial sums and synchronisation words of one call must never leak into
+    the next (the words are compared with each launch's own epoch; partial
+    sums are read only after the other piece of the same call has written
+    them)."""
     log(f"[case] split plan reused workspace Hq{hq} S{s} D{d}")
     ws = None
     for seed in range(3):
@@ -117,8 +117,8 @@ def test_split_plan_reused_workspace(hq, s, d):
 @pytest.mark.parametrize("hq,s,d", [(4, 2048, 128), (2, 1024, 64)])
 def test_split_plan_back_to_back_calls(hq, s, d):
     """Many v2 calls queued on the null stream without synchronisation (one
-    workspace, as a training loop would): each call's preprocess clears the
-    split counters the previous call's main kernel used, so stream order must
+    workspace, as a training loop would): each call's preprocess rewrites the
+    row arrays the previous call's main kernel read, so stream order must
     hold; the last result is bitwise the synchronised one."""
     log(f"[case] back-to-back calls Hq{hq} S{s} D{d}")
     lib = F.load()
@@ -141,6 +141,27 @@ def test_split_plan_back_to_back_calls(hq, s, d):
     torch.cuda.synchronize()
     for n, t in (("dq", dq), ("dk", dk), ("dv", dv)):
         np.testing.assert_array_equal(t.float().cpu().numpy(), ref[n])
+
+
+def test_split_wait_failure_is_reported():
+    """A split job's second piece that gives up waiting for the first piece's
+    partial sums writes the launch's epoch into the workspace's error word,
+    and the synchronised call returns HIP_ERROR instead of a silently wrong
+    sum.  Forced from the host: a spin limit of 0 polls makes every wait give
+    up at once, while every workgroup still runs to its end.  With the
+    default limit back, the next call is correct and reports SUCCESS."""
+    log("[case] split wait gives up (spin limit 0) at P3")
+    lib = F.load()
+    g = O.golden(1, 4, 4, 2048, 128, True)
+    lib.shaobo_fa3_ext_set_split_spin_limit(0)
+    try:
+        res = run_v2(g, torch)
+    finally:
+        lib.shaobo_fa3_ext_set_split_spin_limit(1 << 24)
+    assert res["status"] == F.HIP_ERROR, F.status_name(res["status"])
+    res = run_v2(g, torch)
+    assert res["status"] == F.SUCCESS, F.status_name(res["status"])
+    check(res, g)
 
 
 def test_concurrent_calls_on_two_streams():
@@ -253,55 +274,32 @@ def test_dot_do_o_component(lse_mode):
         np.testing.assert_allclose(pk[:, 1], 1.0 / g["scores_sum"].ravel(), rtol=1e-6)
 
 
-def torch_forward_fill(g, torch, bkv_done):
-    """Fill O/LSE for heads outside the oracle subset with an fp32 torch
-    forward on the GPU (input preparation only)."""
-    B, Hq, S, D = g["q"].shape
-    Hkv = g["k"].shape[1]
-    G = Hq // Hkv
-    out = g["out"].copy()
-    lse = g["lse"].copy()
-    mask = torch.triu(torch.ones(S, S, dtype=torch.bool, device="cuda"), 1)
-    for b in range(B):
-        for h in range(Hq):
-            if bkv_done[0] <= b * Hkv + h // G < bkv_done[1]:
-                continue
-            q = torch.from_numpy(g["q"][b, h]).cuda().float()
-            k = torch.from_numpy(g["k"][b, h // G]).cuda().float()
-            v = torch.from_numpy(g["v"][b, h // G]).cuda().float()
-            s = torch.mm(q, k.t().contiguous()) * g["scale"]
-            if g["causal"]:
-                s.masked_fill_(mask, float("-inf"))
-            l_ = torch.logsumexp(s, -1)
-            out[b, h] = torch.mm(torch.softmax(s, -1), v).half().cpu().numpy()
-            lse[b, h] = l_.cpu().numpy()
-            del s
-    g["out"], g["lse"] = out, lse
-
-
-@pytest.mark.parametrize("B,Hq,Hkv,S,D,causal,bkv", [
-    (2, 32, 8, 4096, 128, True, (9, 10)),    # P4 GQA: oracle on batch 1, kv head 1
-    (2, 16, 16, 8192, 64, False, (31, 32)),  # P5: oracle on batch 1, head 15
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,causal", [
+    (2, 32, 8, 4096, 128, True),    # P4 GQA
+    (2, 16, 16, 8192, 64, False),   # P5
 ])
-def test_full_size_configs(B, Hq, Hkv, S, D, causal, bkv):
-    log(f"[case] full-size B={B} Hq={Hq} Hkv={Hkv} S={S} D={D} causal={causal} oracle bkv={bkv}")
-    g = O.golden(B, Hq, Hkv, S, D, causal, bkv=bkv)
-    torch_forward_fill(g, torch, bkv)
+def test_full_size_configs(B, Hq, Hkv, S, D, causal):
+    """The whole P4 / P5 backward against the oracle (forward and backward
+    on the CPU, about 10 s with 16 threads), checked per (batch, kv-head)
+    group -- dK / dV of the group's KV head, dQ / delta of its query heads,
+    each against its own max|ref| -- so a job-map error confined to some
+    groups cannot hide behind the others' magnitudes (the reference's gate
+    compares whole tensors: src/full_bwd_correctness.cpp:471-500)."""
+    log(f"[case] full-size B={B} Hq={Hq} Hkv={Hkv} S={S} D={D} causal={causal}")
+    g = O.golden(B, Hq, Hkv, S, D, causal)
     res = run_v2(g, torch)
     assert res["status"] == F.SUCCESS
-    G = Hq // Hkv
-    b, hk = divmod(bkv[0], Hkv)
-    qsel = (b, slice(hk * G, hk * G + G))
-    sel = {"delta": qsel, "dq": qsel, "dk": (b, hk), "dv": (b, hk)}
-    rep = check(res, g, sel=sel)
+    rep = check(res, g)
     log({k: round(v["max_rel"], 6) for k, v in rep.items()})
-    # every head: finite, and sum_j dV_j == sum_i dO_i summed over each group
-    for n in ("dq", "dk", "dv", "delta"):
-        assert np.isfinite(res[n]).all(), n
-    sum_dv = res["dv"].astype(np.float64).sum(axis=2)
-    sum_do = g["dout"].astype(np.float64).sum(axis=2).reshape(B, Hkv, G, D).sum(axis=2)
-    err = np.abs(sum_dv - sum_do).max() / np.abs(sum_do).max()
-    assert err < 1e-2, err
+    G = Hq // Hkv
+    worst = {}
+    for b in range(B):
+        for hk in range(Hkv):
+            qsel = (b, slice(hk * G, hk * G + G))
+            sel = {"delta": qsel, "dq": qsel, "dk": (b, hk), "dv": (b, hk)}
+            for n, m in check(res, g, sel=sel).items():
+                worst[n] = max(worst.get(n, 0.0), m["max_rel"])
+    log({"worst group": {k: round(v, 6) for k, v in worst.items()}})
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,S,D,causal", [
