@@ -143,11 +143,13 @@ int finish(hipError_t err, const ShaoboFa3Params* p, hipStream_t stream = nullpt
     return SHAOBO_FA3_STATUS_SUCCESS;
 }
 
-// Shared body of v2 and the legacy entry.
+// Shared body of v2, the legacy entry and the no-allocation entry
+// (no_alloc: the library's static scratch array instead of the caller's
+// workspace, whose fields are then ignored).
 int run_backward(const void* dout, const void* q, const void* k, const void* v, const void* out,
                  const void* aux0, const void* aux1, bool aux_is_lse, void* dq, void* dk,
                  void* dv, void* softmax_d, const ShaoboFa3Params* params,
-                 hipStream_t stream = nullptr) {
+                 hipStream_t stream = nullptr, bool no_alloc = false) {
     const int status = validate(params);
     if (status != SHAOBO_FA3_STATUS_SUCCESS) return status;
     if (dout == nullptr || q == nullptr || k == nullptr || v == nullptr || out == nullptr ||
@@ -157,7 +159,15 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
     }
     const fa3::BwdProblem pr = problem_of(params);
     const fa3::WorkspacePlan plan = fa3::plan_workspace(pr);
-    if (!plan.ok || params->workspace == nullptr || params->workspace_bytes < plan.total) {
+    void* workspace = params->workspace;
+    if (no_alloc) {
+        // shapes whose workspace exceeds the scratch array are refused
+        // before any HIP call
+        if (!plan.ok || plan.total > fa3::kNoAllocScratchBytes) {
+            return SHAOBO_FA3_STATUS_INVALID_VALUE;
+        }
+        if (fa3::noalloc_scratch(&workspace) != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
+    } else if (!plan.ok || workspace == nullptr || params->workspace_bytes < plan.total) {
         return SHAOBO_FA3_STATUS_INVALID_VALUE;
     }
     fa3::BwdTensors t;
@@ -175,8 +185,8 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
     t.delta = static_cast<float*>(softmax_d);
     t.stream = stream;
     unsigned long long epoch = 0;
-    const hipError_t err = fa3::launch_backward(pr, t, params->workspace, &epoch);
-    const char* ws = static_cast<const char*>(params->workspace);
+    const hipError_t err = fa3::launch_backward(pr, t, workspace, &epoch);
+    const char* ws = static_cast<const char*>(workspace);
     return finish(err, params, stream, plan.bal_m > 0 ? ws + plan.err_off : nullptr, epoch);
 }
 
@@ -292,6 +302,14 @@ int shaobo_fa3_bwd_v2_on_stream(const void* dout, const void* q, const void* k, 
 }
 
 void shaobo_fa3_ext_set_split_spin_limit(int polls) { fa3::set_split_spin_limit(polls); }
+
+int shaobo_fa3_ext_bwd_v2_no_alloc(const void* dout, const void* q, const void* k, const void* v,
+                                   const void* out, const void* softmax_lse, void* dq, void* dk,
+                                   void* dv, void* softmax_d, const ShaoboFa3Params* params,
+                                   void* stream) {
+    return run_backward(dout, q, k, v, out, softmax_lse, nullptr, true, dq, dk, dv, softmax_d,
+                        params, static_cast<hipStream_t>(stream), true);
+}
 
 const char* shaobo_fa3_status_string(int status) {
     switch (status) {

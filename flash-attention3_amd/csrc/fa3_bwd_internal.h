@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "shaobo_fa3_ext.h"
+
 namespace fa3 {
 
 // Keys owned by one workgroup of the main kernel, and query rows it consumes
@@ -99,5 +101,11 @@ hipError_t launch_component(const BwdProblem& p, const BwdTensors& t, int role);
 
 // Polls a split wait makes before it gives up (test hook; default 1 << 24).
 void set_split_spin_limit(int polls);
+
+// Workspace of the no-allocation entry: a static device array of
+// kNoAllocScratchBytes per GPU.  noalloc_scratch returns its device address
+// on the current device (looked up once per device, then cached).
+constexpr size_t kNoAllocScratchBytes = SHAOBO_FA3_EXT_SCRATCH_BYTES;
+hipError_t noalloc_scratch(void** ptr);
 
 }  // namespace fa3

@@ -51,6 +51,7 @@
 
 #include <atomic>
 #include <chrono>
+#include <mutex>
 #include <random>
 
 namespace fa3 {
@@ -1432,6 +1433,37 @@ struct Checked {
 }  // namespace
 
 void set_split_spin_limit(int polls) { g_spin_limit.store(polls < 0 ? 0 : polls); }
+
+// Workspace of the no-allocation entry.  Each GPU holds its own copy of the
+// array; in host code `scratch` is only a handle for the runtime, never a
+// device address, so the kernels receive the address hipGetSymbolAddress
+// reports for the current device.  Nothing in it needs clearing between
+// calls: the split words are tagged with each launch's epoch, and everything
+// else is written before it is read within a call.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+hipError_t noalloc_scratch(void** ptr) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // with `dev` current
+        if (e != hipSuccess) return e;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return hipSuccess;
+}
 
 WorkspacePlan plan_workspace(const BwdProblem& p) {
     WorkspacePlan w;

@@ -34,7 +34,12 @@ EXPORTS = (
     "shaobo_fa3_bwd_dkv_workspace_bytes", "shaobo_fa3_bwd_dkv",
     "shaobo_fa3_bwd_dq_workspace_bytes", "shaobo_fa3_bwd_dq",
     "shaobo_fa3_bwd_v2_on_stream", "shaobo_fa3_ext_set_split_spin_limit",
+    "shaobo_fa3_ext_bwd_v2_no_alloc",
 )
+
+# Size of the static device scratch array behind shaobo_fa3_ext_bwd_v2_no_alloc
+# (SHAOBO_FA3_EXT_SCRATCH_BYTES in include/shaobo_fa3_ext.h).
+NO_ALLOC_SCRATCH_BYTES = 32 << 20
 
 # Component path selectors (params.dkv_path / params.dq_path) of the canonical
 # dK/dV and dQ component kernels.
@@ -145,6 +150,9 @@ def load(path=LIB_PATH):
         lib.shaobo_fa3_bwd_dq.restype = ctypes.c_int
         lib.shaobo_fa3_ext_set_split_spin_limit.argtypes = [ctypes.c_int]
         lib.shaobo_fa3_ext_set_split_spin_limit.restype = None
+        lib.shaobo_fa3_ext_bwd_v2_no_alloc.argtypes = [ctypes.c_void_p] * 10 + [
+            ctypes.POINTER(Params), ctypes.c_void_p]
+        lib.shaobo_fa3_ext_bwd_v2_no_alloc.restype = ctypes.c_int
         if path != LIB_PATH:
             return lib
         _LIB = lib

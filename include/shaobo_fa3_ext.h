@@ -43,6 +43,35 @@ int shaobo_fa3_bwd_v2_on_stream(const void* dout,
  * call. */
 void shaobo_fa3_ext_set_split_spin_limit(int polls);
 
+/* Size of the device scratch array behind shaobo_fa3_ext_bwd_v2_no_alloc:
+ * 32 MiB per GPU, held from the library's first use on that GPU until the
+ * process ends. */
+#define SHAOBO_FA3_EXT_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* shaobo_fa3_bwd_v2_on_stream without a workspace: no counterpart in the
+ * reference.  It is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The workspace_bytes / workspace fields of params are ignored;
+ * the library uses a static device array of SHAOBO_FA3_EXT_SCRATCH_BYTES on
+ * the current GPU instead, and calls no hipMalloc / hipFree.  A shape whose
+ * workspace (shaobo_fa3_bwd_v2_workspace_bytes) exceeds that size returns
+ * SHAOBO_FA3_STATUS_INVALID_VALUE before any HIP call.  Inputs, outputs,
+ * statuses and results are those of shaobo_fa3_bwd_v2_on_stream.  Every
+ * call on one GPU shares that GPU's array: calls that may overlap in time on
+ * one GPU (other streams, other host threads) race and must not be made. */
+int shaobo_fa3_ext_bwd_v2_no_alloc(const void* dout,
+                                   const void* q,
+                                   const void* k,
+                                   const void* v,
+                                   const void* out,
+                                   const void* softmax_lse,
+                                   void* dq,
+                                   void* dk,
+                                   void* dv,
+                                   void* softmax_d,
+                                   const ShaoboFa3Params* params,
+                                   void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif
