@@ -2,12 +2,18 @@
 
 A step is one full backward through the C ABI over resident fp16 inputs at
 the headline shape B=1, H=4, S=2048, D=128, causal (BASELINE.json
-configs[2]).  v2 is one kernel launch (the main kernel forms delta and lse2
-itself), so the step's HIP events, recorded on the null stream where the
-library launches, time the main kernel back to back.  Prints one JSON line:
-TFLOP/s from FLOPs = 10*B*H*S^2*D*0.5, ms per backward, % of fp16 dense MFMA
-peak, the main kernel's roofline, and the CPU oracle timed on the host as the
-reported CPU baseline.
+configs[2]): the delta preprocess and the main kernel, two launches on the
+null stream.  The timed region is `steps` back-to-back shaobo_fa3_bwd_v2
+calls between two HIP events.  A second run of as many back-to-back calls,
+through shaobo_fa3_ext_bwd_v2_timed (v2 that also records an event before,
+between and after the two kernels), gives each kernel's average duration in
+the same regime, from which the rooflines are computed.  Each event marker
+delays the next kernel's start by its dispatch latency, which the interval
+then includes, so these per-kernel durations (and the rooflines drawn from
+them) are upper bounds on the pure execution times a kernel trace reports.  Prints one JSON
+line: TFLOP/s from FLOPs = 10*B*H*S^2*D*0.5, ms per backward, % of fp16 dense
+MFMA peak, the main kernel's (MFMA) and the preprocess's (HBM) rooflines,
+and the CPU oracle timed on the host as the reported CPU baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config P3]
 """
@@ -104,10 +110,19 @@ def load_traffic(config):
     return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
+def preprocess_bytes(B, Hq, S, D):
+    """Bytes one preprocess launch must move: read O and dO (fp16) and the
+    LSE row; write delta, lse2 and -delta (fp32) per row."""
+    rows = B * Hq * S
+    return 2 * rows * D * 2 + rows * 4 * 4
+
+
 def cpu_baseline(cfg, budget_s):
-    """Time the CPU oracle's backward (fp32, threaded) on a bounded sample of
-    the same workload: whole (batch, kv-head) groups of the config, repeated
-    until about budget_s seconds of CPU work have run."""
+    """Time the CPU oracle (fp32) on the host: its threaded backward on a
+    bounded sample of the same workload -- whole (batch, kv-head) groups of
+    the config, repeated until about budget_s seconds of CPU work have run --
+    its threaded forward on the same sample, timed separately, and its
+    single-threaded backward of the whole P1, P2 and P3 configs."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import fa3_oracle as O
     B, Hq, Hkv, S, D, causal = cfg
@@ -116,7 +131,9 @@ def cpu_baseline(cfg, budget_s):
     # whole config when small (P1-P3), else one (batch, kv-head) group
     groups = B * Hkv if B * Hq * S <= 8192 else 1
     x = O.make_inputs(B, Hq, Hkv, S, D)
+    t0 = time.perf_counter()
     out, smax, ssum, _ = O.forward(x["q"], x["k"], x["v"], causal, scale, (0, groups), threads)
+    fwd_s = time.perf_counter() - t0
     runs, t_total = 0, 0.0
     while t_total < budget_s or runs == 0:
         t0 = time.perf_counter()
@@ -129,11 +146,24 @@ def cpu_baseline(cfg, budget_s):
     sample_heads = groups * (Hq // Hkv)
     f = flops(1, sample_heads, S, D, causal)
     sec = t_total / runs
+    single = {}
+    for name in ("P1", "P2", "P3"):
+        b1, hq1, hkv1, s1, d1, c1 = CONFIGS[name]
+        x1 = O.make_inputs(b1, hq1, hkv1, s1, d1)
+        sc1 = 1.0 / math.sqrt(d1)
+        o1, m1, l1, _ = O.forward(x1["q"], x1["k"], x1["v"], c1, sc1, None, 1)
+        t0 = time.perf_counter()
+        O.backward(x1["q"], x1["k"], x1["v"], o1, x1["dout"], m1, l1, c1, sc1, None, 1)
+        dt = time.perf_counter() - t0
+        single[name] = {"bwd_ms": round(dt * 1e3, 3),
+                        "tflops": round(flops(b1, hq1, s1, d1, c1) / dt / 1e12, 6)}
     return {"value": round(f / sec / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": f"oracle fp32 backward of {sample_heads} of {B * Hq} query heads "
                       f"(S={S}, D={D}, causal={causal}), {runs} runs, {sec * 1e3:.1f} ms each",
-            "ms_per_bwd_sample": round(sec * 1e3, 3)}
+            "ms_per_bwd_sample": round(sec * 1e3, 3),
+            "fwd_ms_sample": round(fwd_s * 1e3, 3),
+            "single_thread_bwd": single}
 
 
 def main():
@@ -210,9 +240,20 @@ def main():
     f = flops(B, Hq, S, D, causal)
     tflops = f / (ms * 1e-3) / 1e12
 
-    # v2 is one launch per step: the step time is the main kernel's, back to back
-    main_ms = ms
+    # ---- per-kernel durations, back to back: the same number of calls
+    # through the timed entry, three events per call, read after one sync ----
+    evs = [[hip.event() for _ in range(3)] for _ in range(args.steps)]
+    ev_arrays = [(ctypes.c_void_p * 3)(*[e.value for e in trio]) for trio in evs]
+    for i in range(args.steps):
+        st = lib.shaobo_fa3_ext_bwd_v2_timed(*argv, ctypes.byref(p), None, ev_arrays[i])
+        if st != F.SUCCESS:
+            raise RuntimeError("shaobo_fa3_ext_bwd_v2_timed: " + F.status_name(st))
+    torch.cuda.synchronize()
+    pre_ms = sum(hip.elapsed_ms(t[0], t[1]) for t in evs) / args.steps
+    main_ms = sum(hip.elapsed_ms(t[1], t[2]) for t in evs) / args.steps
+    staged_ms = hip.elapsed_ms(evs[0][0], evs[-1][2]) / args.steps
     main_tflops = f / (main_ms * 1e-3) / 1e12
+    pre_gbs = preprocess_bytes(B, Hq, S, D) / (pre_ms * 1e-3) / 1e9
     traffic = load_traffic(args.config)
     result = {
         "metric": METRIC,
@@ -236,12 +277,17 @@ def main():
         "wall_s_timed": round(wall, 4),
         "warmup_steps_run": done,
         "warmup_s": round(warm_s, 3),
-        "kernels_ms": {"bwd_main_kernel": round(main_ms, 5)},
+        "kernels_ms": {"preprocess_kernel": round(pre_ms, 5), "bwd_main_kernel": round(main_ms, 5)},
+        "staged_ms_per_step": round(staged_ms, 5),
         "roofline": {"kernel": "bwd_main_kernel", "bound": "mfma",
                      "achieved": round(main_tflops, 3),
                      "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(main_tflops / FP16_PEAK_TFLOPS, 5),
                      "traffic": traffic},
+        "preprocess_roofline": {"kernel": "preprocess_kernel", "bound": "hbm",
+                                "achieved": round(pre_gbs, 1), "peak": HBM_PEAK_GBS,
+                                "unit": "GB/s", "frac": round(pre_gbs / HBM_PEAK_GBS, 5),
+                                "bytes": preprocess_bytes(B, Hq, S, D)},
     }
     if args.calib_copy_mb > 0:
         # plain copy kernel of known size, for scaling rocprofv3 FETCH/WRITE_SIZE

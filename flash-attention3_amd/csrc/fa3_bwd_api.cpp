@@ -143,13 +143,22 @@ int finish(hipError_t err, const ShaoboFa3Params* p, hipStream_t stream = nullpt
     return SHAOBO_FA3_STATUS_SUCCESS;
 }
 
-// Shared body of v2, the legacy entry and the no-allocation entry
-// (no_alloc: the library's static scratch array instead of the caller's
-// workspace, whose fields are then ignored).
+// Options of the extension entries: the launch stream; no_alloc: the
+// library's static scratch array instead of the caller's workspace, whose
+// fields are then ignored; events: three hipEvent_t recorded around the two
+// kernels (or null).
+struct RunOpts {
+    hipStream_t stream = nullptr;
+    bool no_alloc = false;
+    void* const* events = nullptr;
+};
+
+// Shared body of v2, the legacy entry and the extension entries.
 int run_backward(const void* dout, const void* q, const void* k, const void* v, const void* out,
                  const void* aux0, const void* aux1, bool aux_is_lse, void* dq, void* dk,
                  void* dv, void* softmax_d, const ShaoboFa3Params* params,
-                 hipStream_t stream = nullptr, bool no_alloc = false) {
+                 const RunOpts& opt = RunOpts{}) {
+    const hipStream_t stream = opt.stream;
     const int status = validate(params);
     if (status != SHAOBO_FA3_STATUS_SUCCESS) return status;
     if (dout == nullptr || q == nullptr || k == nullptr || v == nullptr || out == nullptr ||
@@ -160,7 +169,7 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
     const fa3::BwdProblem pr = problem_of(params);
     const fa3::WorkspacePlan plan = fa3::plan_workspace(pr);
     void* workspace = params->workspace;
-    if (no_alloc) {
+    if (opt.no_alloc) {
         // shapes whose workspace exceeds the scratch array are refused
         // before any HIP call
         if (!plan.ok || plan.total > fa3::kNoAllocScratchBytes) {
@@ -184,6 +193,9 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
     t.dv = dv;
     t.delta = static_cast<float*>(softmax_d);
     t.stream = stream;
+    if (opt.events != nullptr) {
+        for (int i = 0; i < 3; ++i) t.events[i] = static_cast<hipEvent_t>(opt.events[i]);
+    }
     unsigned long long epoch = 0;
     const hipError_t err = fa3::launch_backward(pr, t, workspace, &epoch);
     const char* ws = static_cast<const char*>(workspace);
@@ -297,8 +309,10 @@ int shaobo_fa3_bwd_v2_on_stream(const void* dout, const void* q, const void* k, 
                                 const void* out, const void* softmax_lse, void* dq, void* dk,
                                 void* dv, void* softmax_d, const ShaoboFa3Params* params,
                                 void* stream) {
+    RunOpts opt;
+    opt.stream = static_cast<hipStream_t>(stream);
     return run_backward(dout, q, k, v, out, softmax_lse, nullptr, true, dq, dk, dv, softmax_d,
-                        params, static_cast<hipStream_t>(stream));
+                        params, opt);
 }
 
 void shaobo_fa3_ext_set_split_spin_limit(int polls) { fa3::set_split_spin_limit(polls); }
@@ -307,8 +321,22 @@ int shaobo_fa3_ext_bwd_v2_no_alloc(const void* dout, const void* q, const void* 
                                    const void* out, const void* softmax_lse, void* dq, void* dk,
                                    void* dv, void* softmax_d, const ShaoboFa3Params* params,
                                    void* stream) {
+    RunOpts opt;
+    opt.stream = static_cast<hipStream_t>(stream);
+    opt.no_alloc = true;
     return run_backward(dout, q, k, v, out, softmax_lse, nullptr, true, dq, dk, dv, softmax_d,
-                        params, static_cast<hipStream_t>(stream), true);
+                        params, opt);
+}
+
+int shaobo_fa3_ext_bwd_v2_timed(const void* dout, const void* q, const void* k, const void* v,
+                                const void* out, const void* softmax_lse, void* dq, void* dk,
+                                void* dv, void* softmax_d, const ShaoboFa3Params* params,
+                                void* stream, void* const* events) {
+    RunOpts opt;
+    opt.stream = static_cast<hipStream_t>(stream);
+    opt.events = events;
+    return run_backward(dout, q, k, v, out, softmax_lse, nullptr, true, dq, dk, dv, softmax_d,
+                        params, opt);
 }
 
 const char* shaobo_fa3_status_string(int status) {

@@ -53,6 +53,9 @@ struct BwdTensors {
     // Stream of every launch (null: the legacy default stream, as in the
     // reference ABI; the stream entry points pass the caller's).
     hipStream_t stream = nullptr;
+    // Optional events recorded on `stream` before the preprocess, before the
+    // main kernel and after it (null: not recorded).
+    hipEvent_t events[3] = {nullptr, nullptr, nullptr};
 };
 
 // Device workspace of the v2 / legacy / fused5 entries (regions 256-B

@@ -1527,8 +1527,14 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     FusedArgs a = base_args(p, t);
     float* lse2 = reinterpret_cast<float*>(ws + plan.lse2_off);
     float* ndelta = reinterpret_cast<float*>(ws + plan.ndelta_off);
-    const hipError_t err = t.packed_in != nullptr ? launch_rowstats(p, t, lse2, ndelta)
-                                                  : launch_preprocess(p, t, lse2, ndelta);
+    auto mark = [&](int i) {
+        return t.events[i] != nullptr ? hipEventRecord(t.events[i], t.stream) : hipSuccess;
+    };
+    hipError_t err = mark(0);
+    if (err != hipSuccess) return err;
+    err = t.packed_in != nullptr ? launch_rowstats(p, t, lse2, ndelta)
+                                 : launch_preprocess(p, t, lse2, ndelta);
+    if (err == hipSuccess) err = mark(1);
     if (err != hipSuccess) return err;
     a.lse2 = lse2;
     a.ndelta = ndelta;
@@ -1551,7 +1557,8 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     }
     if (p.head_dim == 128) launch_d<128>(a, p.causal, p.bf16, t.stream);
     else launch_d<64>(a, p.causal, p.bf16, t.stream);
-    return hipGetLastError();
+    err = hipGetLastError();
+    return err == hipSuccess ? mark(2) : err;
 }
 
 }  // namespace fa3

@@ -34,7 +34,7 @@ EXPORTS = (
     "shaobo_fa3_bwd_dkv_workspace_bytes", "shaobo_fa3_bwd_dkv",
     "shaobo_fa3_bwd_dq_workspace_bytes", "shaobo_fa3_bwd_dq",
     "shaobo_fa3_bwd_v2_on_stream", "shaobo_fa3_ext_set_split_spin_limit",
-    "shaobo_fa3_ext_bwd_v2_no_alloc",
+    "shaobo_fa3_ext_bwd_v2_no_alloc", "shaobo_fa3_ext_bwd_v2_timed",
 )
 
 # Size of the static device scratch array behind shaobo_fa3_ext_bwd_v2_no_alloc
@@ -153,6 +153,9 @@ def load(path=LIB_PATH):
         lib.shaobo_fa3_ext_bwd_v2_no_alloc.argtypes = [ctypes.c_void_p] * 10 + [
             ctypes.POINTER(Params), ctypes.c_void_p]
         lib.shaobo_fa3_ext_bwd_v2_no_alloc.restype = ctypes.c_int
+        lib.shaobo_fa3_ext_bwd_v2_timed.argtypes = [ctypes.c_void_p] * 10 + [
+            ctypes.POINTER(Params), ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+        lib.shaobo_fa3_ext_bwd_v2_timed.restype = ctypes.c_int
         if path != LIB_PATH:
             return lib
         _LIB = lib

@@ -43,6 +43,26 @@ int shaobo_fa3_bwd_v2_on_stream(const void* dout,
  * call. */
 void shaobo_fa3_ext_set_split_spin_limit(int polls);
 
+/* shaobo_fa3_bwd_v2_on_stream that also records three caller-created
+ * hipEvent_t on `stream`: events[0] before the delta preprocess, events[1]
+ * between it and the main kernel, events[2] after the main kernel (a NULL
+ * handle is skipped).  No counterpart in the reference; it is for
+ * benchmarks that time each kernel inside a run of back-to-back calls
+ * (bench.py).  Everything else is shaobo_fa3_bwd_v2_on_stream's. */
+int shaobo_fa3_ext_bwd_v2_timed(const void* dout,
+                                const void* q,
+                                const void* k,
+                                const void* v,
+                                const void* out,
+                                const void* softmax_lse,
+                                void* dq,
+                                void* dk,
+                                void* dv,
+                                void* softmax_d,
+                                const ShaoboFa3Params* params,
+                                void* stream,
+                                void* const* events);
+
 /* Size of the device scratch array behind shaobo_fa3_ext_bwd_v2_no_alloc:
  * 32 MiB per GPU, held from the library's first use on that GPU until the
  * process ends. */
