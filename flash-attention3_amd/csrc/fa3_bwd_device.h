@@ -52,34 +52,28 @@ __device__ __forceinline__ float dot8(f16x8 a, f16x8 b, float acc) {
     return acc;
 }
 
-// 16-byte chunk of D that lane group g (of 4 per row) takes in k-step s of
-// a 16x16x32 MFMA operand read from a [rows][D] tile: the main kernel's
-// order (with the tile swizzle of tile_off<D> every ds_read_b128 is then
-// conflict-free; the order 4 s + g would put two lanes of a group on one
-// bank quad).  The delta sums below follow it, so that delta formed in the
-// main kernel and by the preprocess pass agree bit for bit.
+// 16-byte chunk of D that lane group g4 (= lane / 16) reads in k-step s of
+// a 16x16x32 MFMA operand taken from 16 consecutive rows of a [64][D] tile.
+// ds_read_b128 serves a wave in four groups of 16 lanes, lane l belonging to
+// group (l / 32, parity of bits 2..4 of l); with the tile swizzle of
+// tile_off<D> these orders give every group 16 distinct bank quads (the
+// order 4 s + g4 would put two lanes of a group on one quad).
 template <int D>
-__device__ __forceinline__ int p1_chunk(int s, int g) {
-    if constexpr (D == 128) return s + 4 * g;
-    else return s + 2 * (g >> 1) + 4 * (g & 1);
+__device__ __forceinline__ int p1_chunk(int s, int g4) {
+    if constexpr (D == 128) return s + 4 * g4;
+    else return s + 2 * (g4 >> 1) + 4 * (g4 & 1);
 }
 
 // delta = sum_d fp32(dO[row, d]) * fp32(O[row, d]) of one query row whose
-// elements start at `elem`, formed by 4 lanes (g = lane % 4 of 4 consecutive
-// lanes): lane g sums chunks p1_chunk(s, g), s = 0 .. D / 32 - 1, with dot8,
-// then the pairs (g0, g1), (g2, g3) are added and then the two halves --
-// the order in which the main kernel adds its lane groups.
+// elements start at `elem`: lane `sub` of the row's D / 8 consecutive lanes
+// takes the 16-byte chunk sub (dot8), then a butterfly over those lanes.
 template <int D, bool kBf16 = false>
-__device__ __forceinline__ float row_delta4(const _Float16* dout, const _Float16* out, size_t elem,
-                                            int g) {
-    float acc = 0.f;
+__device__ __forceinline__ float row_delta(const _Float16* dout, const _Float16* out, size_t elem,
+                                           int sub) {
+    const size_t c = elem + (size_t)sub * 8;
+    float acc = dot8<kBf16>(*(const f16x8*)(dout + c), *(const f16x8*)(out + c), 0.f);
 #pragma unroll
-    for (int s = 0; s < D / 32; ++s) {
-        const size_t c = elem + (size_t)p1_chunk<D>(s, g) * 8;
-        acc = dot8<kBf16>(*(const f16x8*)(dout + c), *(const f16x8*)(out + c), acc);
-    }
-    acc += __shfl_xor(acc, 1, 4);
-    acc += __shfl_xor(acc, 2, 4);
+    for (int off = D / 16; off > 0; off >>= 1) acc += __shfl_xor(acc, off, D / 8);
     return acc;
 }
 

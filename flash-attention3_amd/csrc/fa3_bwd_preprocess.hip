@@ -11,9 +11,9 @@
 // Optionally also writes the reference's packed sidecar
 // [row_max_log2, row_inv_sum, delta] (reference src/dot_do_o_kernel.cpp:49-61).
 //
-// HBM-bound: 4 lanes per row, D / 32 16-byte loads of dO and of O per lane,
-// in-register dots and a 2-step butterfly over the row's lanes, in the order
-// the main kernel forms delta inline (row_delta4), so both agree bit for bit.
+// HBM-bound: D / 8 lanes per row, each with one 16-byte load of dO and one of
+// O (so every load of the launch is in flight at once), an in-register dot and
+// a butterfly over the row's lanes (row_delta).
 #include "fa3_bwd_device.h"
 #include "fa3_bwd_internal.h"
 
@@ -29,7 +29,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     float* __restrict__ delta, float* __restrict__ lse2, float* __restrict__ ndelta,
     float* __restrict__ packed, int rows,
     float scale_log2, int heads_q, int seqlen, int q_rs, int q_hs) {
-    constexpr int kLanesPerRow = 4;
+    constexpr int kLanesPerRow = D / 8;
     constexpr int kRowsPerBlock = 256 / kLanesPerRow;
     const int sub = threadIdx.x % kLanesPerRow;
     const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
@@ -38,7 +38,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const int hs = heads_q * seqlen;
     const int b = row / hs, rem = row - b * hs, h = rem / seqlen, sq = rem - h * seqlen;
     const size_t elem = (size_t)b * hs * D + (size_t)h * q_hs + (size_t)sq * q_rs;
-    const float acc = row_delta4<D, kBf16>(dout, out, elem, sub);
+    const float acc = row_delta<D, kBf16>(dout, out, elem, sub);
 
     if (sub == 0) {
         float l2, max_log2, inv_sum;
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
 
 template <int D>
 hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta) {
-    constexpr int kRowsPerBlock = 256 / 4;
+    constexpr int kRowsPerBlock = 256 / (D / 8);
     const int rows = p.batch * p.heads_q * p.seqlen;
     const int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
     const float scale_log2 = p.scale * kLog2e;
