@@ -213,6 +213,7 @@ size_t workspace_bytes_of(const ShaoboFa3Params* params) {
 // Reference path ids (include/dkv_contract.h:7-8, include/dq_contract.h:7-8).
 constexpr int kDkvPathCanonical = 5;
 constexpr int kDqPathCanonical = 6;
+constexpr int kPathReferenceCorrectness = 1;  // naive path of both components
 
 // Shape / dtype / layout acceptance shared by the dKV and dQ components
 // (reference valid_dkv_shape / valid_dq_shape, src/dkv_kernel.cpp:50-57,
@@ -224,6 +225,62 @@ bool component_shape_ok(const ShaoboFa3Params* p) {
            p->dtype == SHAOBO_FA3_DTYPE_FP16 && p->layout == SHAOBO_FA3_LAYOUT_BHSD &&
            p->seqlen_k == p->seqlen_q && p->seqlen_q % kSequenceAlignment == 0 &&
            p->num_heads_kv == p->num_heads_q && p->causal == 1;
+}
+
+// Acceptance of the naive path 1 (reference valid_reference_shape,
+// src/dkv_kernel.cpp:69-75, src/dq_kernel.cpp:72-78): fp16 BHSD, Sq == Sk,
+// one query head per KV head, no dropout; any sequence length and causal
+// flag.  The reference builds D = 128 only; D = 64 is accepted here too.
+bool naive_shape_ok(const ShaoboFa3Params* p) {
+    return p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0 && p->num_heads_q > 0 &&
+           head_dim_supported(p->head_dim_qk) && p->head_dim_v == p->head_dim_qk &&
+           p->dtype == SHAOBO_FA3_DTYPE_FP16 && p->layout == SHAOBO_FA3_LAYOUT_BHSD &&
+           p->seqlen_k == p->seqlen_q && p->num_heads_kv == p->num_heads_q &&
+           p->dropout_p == 0.0f;
+}
+
+// Workspace of path 1 (reference reference_workspace_bytes,
+// src/dkv_kernel.cpp:77-86): (2 B H S^2 + 3 B H S) fp32; 0 for other shapes.
+size_t naive_workspace(const ShaoboFa3Params* p) {
+    if (!naive_shape_ok(p)) return 0;
+    fa3::BwdProblem pr;
+    pr.batch = p->batch;
+    pr.seqlen = p->seqlen_q;
+    pr.heads_q = p->num_heads_q;
+    pr.heads_kv = p->num_heads_kv;
+    pr.head_dim = p->head_dim_qk;
+    return fa3::naive_workspace_bytes(pr);
+}
+
+// Path 1 of either component (reference src/dkv_kernel.cpp:1320-1372,
+// src/dq_kernel.cpp:1562-1625): role 1 writes fp32 dK / dV, role 2 fp32 dQ.
+int run_naive(const void* dout, const void* q, const void* k, const void* v, void* dq,
+              void* dk, void* dv, const ShaoboFa3Params* params, int role) {
+    if (!naive_shape_ok(params)) return SHAOBO_FA3_STATUS_UNSUPPORTED;
+    const bool outs = role == 1 ? (dk != nullptr && dv != nullptr) : dq != nullptr;
+    if (dout == nullptr || q == nullptr || k == nullptr || v == nullptr || !outs ||
+        params->workspace == nullptr) {
+        return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    }
+    const size_t need = naive_workspace(params);
+    if (need == 0 || params->workspace_bytes < need) return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    fa3::BwdProblem pr;
+    pr.batch = params->batch;
+    pr.seqlen = params->seqlen_q;
+    pr.heads_q = params->num_heads_q;
+    pr.heads_kv = params->num_heads_kv;
+    pr.head_dim = params->head_dim_qk;
+    pr.causal = params->causal != 0;
+    pr.scale = params->softmax_scale;
+    fa3::BwdTensors t;
+    t.dout = dout;
+    t.q = q;
+    t.k = k;
+    t.v = v;
+    t.dq = dq;
+    t.dk = dk;
+    t.dv = dv;
+    return finish(fa3::launch_naive(pr, t, params->workspace, role), params);
 }
 
 // fused5 acceptance (reference src/fused_bwd_kernel.cpp:1682-1693): fp16 BHSD,
@@ -440,8 +497,9 @@ int shaobo_fa3_bwd_fused5(const void* dout, const void* q, const void* k, const 
 }
 
 size_t shaobo_fa3_bwd_dkv_workspace_bytes(const ShaoboFa3Params* params) {
-    (void)params;
-    return 0;  // the canonical path reads the sidecar directly
+    // the canonical path reads the sidecar directly and needs none
+    if (params == nullptr || params->dkv_path != kPathReferenceCorrectness) return 0;
+    return naive_workspace(params);
 }
 
 int shaobo_fa3_bwd_dkv(const void* dout, const void* q, const void* k, const void* v,
@@ -452,6 +510,9 @@ int shaobo_fa3_bwd_dkv(const void* dout, const void* q, const void* k, const voi
     (void)softmax_aux1;
     (void)dq;
     if (params == nullptr) return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    if (params->dkv_path == kPathReferenceCorrectness) {
+        return run_naive(dout, q, k, v, nullptr, dk, dv, params, 1);
+    }
     if (params->dkv_path != kDkvPathCanonical || !component_shape_ok(params)) {
         return SHAOBO_FA3_STATUS_UNSUPPORTED;
     }
@@ -471,8 +532,9 @@ int shaobo_fa3_bwd_dkv(const void* dout, const void* q, const void* k, const voi
 }
 
 size_t shaobo_fa3_bwd_dq_workspace_bytes(const ShaoboFa3Params* params) {
-    (void)params;
-    return 0;  // the canonical path reads max / sum / delta directly
+    // the canonical path reads max / sum / delta directly and needs none
+    if (params == nullptr || params->dq_path != kPathReferenceCorrectness) return 0;
+    return naive_workspace(params);
 }
 
 int shaobo_fa3_bwd_dq(const void* dout, const void* q, const void* k, const void* v,
@@ -482,6 +544,9 @@ int shaobo_fa3_bwd_dq(const void* dout, const void* q, const void* k, const void
     (void)dk;
     (void)dv;
     if (params == nullptr) return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    if (params->dq_path == kPathReferenceCorrectness) {
+        return run_naive(dout, q, k, v, dq, nullptr, nullptr, params, 2);
+    }
     if (params->dq_path != kDqPathCanonical || !component_shape_ok(params)) {
         return SHAOBO_FA3_STATUS_UNSUPPORTED;
     }

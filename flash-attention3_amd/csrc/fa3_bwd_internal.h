@@ -102,6 +102,13 @@ hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* lse2
 // writes dQ from aux0 (raw max), aux1 (sum) and t.delta_in.
 hipError_t launch_component(const BwdProblem& p, const BwdTensors& t, int role);
 
+// Naive fp32 correctness path of the dK/dV (role 1) and dQ (role 2)
+// components (dkv_path / dq_path 1): fp16 BHSD, one query head per KV head,
+// fp32 outputs, through the reference's S^2-sized workspace of
+// naive_workspace_bytes(p) bytes (0: the sizes overflow).
+size_t naive_workspace_bytes(const BwdProblem& p);
+hipError_t launch_naive(const BwdProblem& p, const BwdTensors& t, void* workspace, int role);
+
 // Polls a split wait makes before it gives up (test hook; default 1 << 24).
 void set_split_spin_limit(int polls);
 

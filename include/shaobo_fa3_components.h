@@ -48,15 +48,18 @@ int shaobo_fa3_bwd_fused5(const void* dout,
                           void* dv,
                           const ShaoboFa3Params* params);
 
-/* dK / dV only, canonical path (params->dkv_path == 5; reference
- * include/shaobo_fa3_components.h:10-22, src/dkv_kernel.cpp:1300-1421): the
- * packed sidecar of shaobo_fa3_bwd_dot_do_o in params->reserved_ptr[3];
- * dk, dv written as fp32 [B, H, S, D]; out, aux0, aux1 and dq are unused.
- * One query head per KV head, causal, Sq == Sk, Sq % 128 == 0, fp16 BHSD,
- * D in {64, 128}; other shapes and other dkv_path values are UNSUPPORTED
- * (the reference's dkv_path 1 -- a naive kernel that recomputes the forward
- * softmax from Q and K -- is not provided).  No workspace: the workspace-bytes
- * query returns 0, as the reference's does for the canonical path. */
+/* dK / dV only (reference include/shaobo_fa3_components.h:10-22,
+ * src/dkv_kernel.cpp:1288-1421); dk, dv written as fp32 [B, H, S, D].
+ *   dkv_path 5 (canonical): the packed sidecar of shaobo_fa3_bwd_dot_do_o in
+ *     params->reserved_ptr[3]; out, aux0, aux1 and dq unused.  One query head
+ *     per KV head, causal, Sq == Sk, Sq % 128 == 0, fp16 BHSD, D in {64, 128}.
+ *     No workspace: the workspace-bytes query returns 0.
+ *   dkv_path 1 (naive correctness path): recomputes the forward softmax and
+ *     delta from Q, K, V, dO in fp32 (out, aux0, aux1, dq unused) through a
+ *     workspace of (2 B H S^2 + 3 B H S) floats, which the workspace-bytes
+ *     query returns.  One query head per KV head, Sq == Sk (any length),
+ *     either causal flag, fp16 BHSD, no dropout, D in {64, 128}.
+ * Other shapes and other dkv_path values are UNSUPPORTED. */
 size_t shaobo_fa3_bwd_dkv_workspace_bytes(const ShaoboFa3Params* params);
 
 int shaobo_fa3_bwd_dkv(const void* dout,
@@ -71,12 +74,15 @@ int shaobo_fa3_bwd_dkv(const void* dout,
                        void* dv,
                        const ShaoboFa3Params* params);
 
-/* dQ only, canonical path (params->dq_path == 6; reference
- * include/shaobo_fa3_components.h:24-36, src/dq_kernel.cpp:1497-1554):
- * aux0 = raw row max, aux1 = row sum (SMAX_SSUM convention), delta in
- * params->reserved_ptr[0]; dq written as fp32 [B, Hq, S, D]; out, dk, dv
- * unused.  Shapes as for shaobo_fa3_bwd_dkv; dq_path 1 is not provided.
- * No workspace (the workspace-bytes query returns 0). */
+/* dQ only (reference include/shaobo_fa3_components.h:24-36,
+ * src/dq_kernel.cpp:1486-1625); dq written as fp32 [B, Hq, S, D]; out, dk,
+ * dv unused.
+ *   dq_path 6 (canonical): aux0 = raw row max, aux1 = row sum (SMAX_SSUM
+ *     convention), delta in params->reserved_ptr[0]; shapes as for
+ *     shaobo_fa3_bwd_dkv's canonical path; no workspace.
+ *   dq_path 1 (naive correctness path): as dkv_path 1 (aux0 / aux1 unused),
+ *     with the same workspace size.
+ * Other shapes and other dq_path values are UNSUPPORTED. */
 size_t shaobo_fa3_bwd_dq_workspace_bytes(const ShaoboFa3Params* params);
 
 int shaobo_fa3_bwd_dq(const void* dout,

@@ -347,15 +347,38 @@ def component_params(lib, **kw):
     return p
 
 
+def naive_bytes(batch, heads, seqlen):
+    """Workspace of the naive path 1 (reference reference_workspace_bytes,
+    src/dkv_kernel.cpp:77-86): fp32 prob and dP [rows][S], then row max,
+    row sum and delta [rows]."""
+    rows = batch * heads * seqlen
+    return (2 * rows * seqlen + 3 * rows) * 4
+
+
 def test_component_workspace_sizes(lib):
-    """dkv / dq need no workspace (as the reference's canonical paths,
-    src/dkv_kernel.cpp:1289-1298, src/dq_kernel.cpp:1486-1495); fused5 needs
-    the v2 plan plus the lse2 / -delta arrays its sidecar is folded into, 0
-    for an unsupported shape."""
-    for f in ("dkv", "dq"):
+    """dkv / dq need no workspace on their canonical paths and the S^2-sized
+    one on path 1 (as the reference, src/dkv_kernel.cpp:1289-1298,
+    src/dq_kernel.cpp:1486-1495); fused5 needs the v2 plan, 0 for an
+    unsupported shape."""
+    for f, attr in (("dkv", "dkv_path"), ("dq", "dq_path")):
         fn = getattr(lib, f"shaobo_fa3_bwd_{f}_workspace_bytes")
         assert fn(ctypes.byref(component_params(lib))) == 0
         assert fn(None) == 0
+        p = component_params(lib)
+        setattr(p, attr, 1)
+        assert fn(ctypes.byref(p)) == naive_bytes(1, 2, 256)
+        p = component_params(lib, batch=2, seqlen=200, heads_q=3, causal=False)
+        setattr(p, attr, 1)  # any length, either causal flag
+        assert fn(ctypes.byref(p)) == naive_bytes(2, 3, 200)
+        for name, mut in [("num_heads_kv", 1), ("seqlen_k", 128), ("dtype", F.DTYPE_BF16),
+                          ("layout", F.LAYOUT_BSHD), ("head_dim_qk", 96), ("dropout_p", 0.1)]:
+            p = component_params(lib)
+            setattr(p, attr, 1)
+            setattr(p, name, mut)
+            assert fn(ctypes.byref(p)) == 0, (f, name)
+        p = component_params(lib, batch=1 << 20, seqlen=1 << 20, heads_q=1 << 10)
+        setattr(p, attr, 1)
+        assert fn(ctypes.byref(p)) == 0  # overflows
     ws5 = lib.shaobo_fa3_bwd_fused5_workspace_bytes
     assert ws5(None) == 0
     assert ws5(ctypes.byref(component_params(lib, seqlen=2048, heads_q=4))) == \
@@ -375,13 +398,13 @@ def test_component_error_paths_without_gpu(lib):
     src/fused_bwd_kernel.cpp:1682-1703); every case returns before a launch."""
     one = ctypes.c_void_p(16)
     ten = [one] * 10
-    for name, mut in [("dkv_path", 1), ("causal", 0), ("num_heads_kv", 1), ("head_dim_qk", 96),
+    for name, mut in [("dkv_path", 2), ("causal", 0), ("num_heads_kv", 1), ("head_dim_qk", 96),
                       ("seqlen_q", 200), ("dtype", F.DTYPE_BF16), ("layout", F.LAYOUT_BSHD)]:
         p = component_params(lib)
         p.reserved_ptr[3] = 16
         setattr(p, name, mut)
         assert lib.shaobo_fa3_bwd_dkv(*ten, ctypes.byref(p)) == F.UNSUPPORTED, name
-    for name, mut in [("dq_path", 1), ("dq_path", 5), ("causal", 0), ("seqlen_k", 512)]:
+    for name, mut in [("dq_path", 2), ("dq_path", 5), ("causal", 0), ("seqlen_k", 512)]:
         p = component_params(lib)
         p.reserved_ptr[0] = 16
         setattr(p, name, mut)
@@ -416,3 +439,33 @@ def test_component_error_paths_without_gpu(lib):
     p.workspace, p.workspace_bytes = None, 1 << 30
     assert lib.shaobo_fa3_bwd_fused5(*eight, ctypes.byref(p)) == F.INVALID_VALUE
     assert lib.shaobo_fa3_bwd_fused5(*eight, None) == F.INVALID_VALUE
+
+
+def test_naive_path_error_paths_without_gpu(lib):
+    """Path 1 of dkv / dq (reference src/dkv_kernel.cpp:1320-1334,
+    src/dq_kernel.cpp:1562-1574): shape checks -> UNSUPPORTED, then missing
+    pointers, a missing or short workspace -> INVALID_VALUE; every case
+    returns before a launch."""
+    one = ctypes.c_void_p(16)
+    ten = [one] * 10
+    need = naive_bytes(1, 2, 256)
+    for fn, attr, out_idx in ((lib.shaobo_fa3_bwd_dkv, "dkv_path", 8),
+                              (lib.shaobo_fa3_bwd_dq, "dq_path", 7)):
+        for name, mut in [("num_heads_kv", 1), ("seqlen_k", 128), ("dtype", F.DTYPE_BF16),
+                          ("layout", F.LAYOUT_BSHD), ("dropout_p", 0.1), ("head_dim_qk", 96)]:
+            p = component_params(lib)
+            setattr(p, attr, 1)
+            setattr(p, name, mut)
+            assert fn(*ten, ctypes.byref(p)) == F.UNSUPPORTED, (attr, name)
+        p = component_params(lib)
+        setattr(p, attr, 1)
+        assert fn(*ten, ctypes.byref(p)) == F.INVALID_VALUE  # no workspace
+        p.workspace, p.workspace_bytes = 16, need - 4
+        assert fn(*ten, ctypes.byref(p)) == F.INVALID_VALUE  # short workspace
+        p.workspace_bytes = need
+        bad = list(ten)
+        bad[out_idx] = None
+        assert fn(*bad, ctypes.byref(p)) == F.INVALID_VALUE  # dk / dq missing
+        bad = list(ten)
+        bad[1] = None
+        assert fn(*bad, ctypes.byref(p)) == F.INVALID_VALUE  # q missing

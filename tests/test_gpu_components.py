@@ -8,6 +8,9 @@ the reference's own harness chains them.
   them.
 * shaobo_fa3_bwd_fused5 from a dot_do_o sidecar of either aux convention
   (reference tests/fused_bwd_correctness.cpp:240-262), fp16 outputs.
+* the naive path 1 of shaobo_fa3_bwd_dkv / shaobo_fa3_bwd_dq (reference
+  src/dkv_kernel.cpp:1320-1383, src/dq_kernel.cpp:1562-1625), which
+  recomputes the forward from Q, K, V through an S^2-sized workspace.
 
 Bar: max|err|/max|ref| <= 1e-2 against the oracle's fp32 gradients.
 """
@@ -134,3 +137,38 @@ def test_fused5_matches_v2_bitwise():
     torch.cuda.synchronize()
     for a, b in ((dq, dq2), (dk, dk2), (dv, dv2)):
         np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy())
+
+
+@pytest.mark.parametrize("B,H,S,D,causal", [(1, 2, 128, 128, True), (1, 1, 256, 128, False),
+                                             (2, 1, 200, 128, True), (1, 2, 96, 64, False)])
+def test_naive_path_1(B, H, S, D, causal):
+    """dkv_path 1 -> fp32 dK / dV and dq_path 1 -> fp32 dQ, each through its
+    own S^2-sized workspace (poisoned first), against the oracle; any
+    sequence length (no tile alignment), either causal flag."""
+    log(f"[case] naive path 1 B={B} H={H} S={S} D={D} causal={causal}")
+    lib = F.load()
+    g = O.golden(B, H, H, S, D, causal)
+    p = F.make_params(lib, batch=B, seqlen=S, heads_q=H, head_dim=D, causal=causal,
+                      softmax_scale=g["scale"], sync=True)
+    p.dkv_path, p.dq_path = 1, 1
+    nbytes = lib.shaobo_fa3_bwd_dkv_workspace_bytes(ctypes.byref(p))
+    rows = B * H * S
+    assert nbytes == (2 * rows * S + 3 * rows) * 4
+    assert lib.shaobo_fa3_bwd_dq_workspace_bytes(ctypes.byref(p)) == nbytes
+    ws = torch.full((nbytes,), 0xC3, dtype=torch.uint8, device="cuda")
+    p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
+    q, k, v, do, out = (dev(g[n], torch) for n in ("q", "k", "v", "dout", "out"))
+    dq = torch.full(q.shape, float("nan"), dtype=torch.float32, device="cuda")
+    dk = torch.full(k.shape, float("nan"), dtype=torch.float32, device="cuda")
+    dv = torch.full(v.shape, float("nan"), dtype=torch.float32, device="cuda")
+    st = lib.shaobo_fa3_bwd_dkv(c(do), c(q), c(k), c(v), c(out), None, None, None, c(dk), c(dv),
+                                ctypes.byref(p))
+    assert st == F.SUCCESS, F.status_name(st)
+    ws.fill_(0xC3)
+    st = lib.shaobo_fa3_bwd_dq(c(do), c(q), c(k), c(v), c(out), None, None, c(dq), None, None,
+                               ctypes.byref(p))
+    assert st == F.SUCCESS, F.status_name(st)
+    torch.cuda.synchronize()
+    res = {n: x.cpu().numpy() for n, x in (("dq", dq), ("dk", dk), ("dv", dv))}
+    rep = check(res, g, names=("dq", "dk", "dv"))
+    log({n: round(m["max_rel"], 6) for n, m in rep.items()})
