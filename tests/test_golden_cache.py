@@ -120,3 +120,65 @@ def test_command_line_tool(tmp_path):
     assert "golden_cache_status=MISS" in out1 and "golden_cache_status=HIT" in out2
     digest = [line for line in out1.splitlines() if line.startswith("golden_payload_sha256=")]
     assert digest and digest[0] in out2
+
+
+# ---- caches written by the reference's own tool ----------------------------
+# Fixtures made by tests/golden/make_reference_caches.py, which runs the
+# reference's scripts/generate_full_bwd_golden.py (build container only).
+REF_CACHES = os.path.join(HERE, "golden", "reference_caches")
+REF_SHAPES = [dict(batch=1, heads_q=1, heads_kv=1, seqlen=128, head_dim=128),
+              dict(batch=1, heads_q=4, heads_kv=2, seqlen=128, head_dim=128)]
+
+
+def ref_cache(dims, causal=1):
+    return os.path.join(REF_CACHES, GC.cache_key(causal=causal, **dims))
+
+
+@pytest.mark.parametrize("dims", REF_SHAPES, ids=["mha", "gqa"])
+def test_reference_tool_cache_is_read(dims):
+    """The reference tool's cache sits under the directory name cache_key
+    computes, and validate / read accept it unchanged (manifest contract,
+    file set, dtypes, shapes, per-file and payload SHA-256)."""
+    path = ref_cache(dims)
+    assert os.path.isdir(path), path
+    GC.validate(path, causal=1, **dims)
+    a = GC.read(path, causal=1, **dims)
+    assert set(a) == set(GC.file_specs(**dims))
+    # its packed sidecar is the one golden_cache derives from the row stats
+    want = GC.packed_sidecar(a["scores_max.f32"], a["scores_sum.f32"], a["delta.f32"],
+                             GC.DEFAULT_SCALE)
+    np.testing.assert_array_equal(a["packed_sidecar.f32"], want)
+
+
+@pytest.mark.parametrize("dims", REF_SHAPES, ids=["mha", "gqa"])
+def test_our_writer_reproduces_reference_cache(tmp_path, dims):
+    """golden_cache.write, given the reference cache's arrays, writes the same
+    bytes: identical per-file SHA-256, payload digest and manifest."""
+    a = GC.read(ref_cache(dims), causal=1, **dims)
+    ours = GC.write(tmp_path, a, causal=1, **dims)
+    theirs = json.loads(open(os.path.join(ref_cache(dims), "manifest.json")).read())
+    mine = json.loads((ours / "manifest.json").read_text())
+    assert mine == theirs
+
+
+@pytest.mark.parametrize("dims", REF_SHAPES, ids=["mha", "gqa"])
+def test_oracle_against_reference_cache(dims):
+    """The oracle on the reference's deterministic pattern: its inputs equal
+    the cache's .f16 files bit for bit, and its outputs meet the reference's
+    own gates (src/full_bwd_correctness.cpp:471-500) and the north-star bar
+    against the tool's fp32 results; O differs by at most one fp16 ulp and the
+    row statistics agree to fp32 rounding (numpy sums in another order)."""
+    import fa3_oracle as O
+    a = GC.read(ref_cache(dims), causal=1, **dims)
+    B, Hq, Hkv, S, D = (dims[k] for k in ("batch", "heads_q", "heads_kv", "seqlen", "head_dim"))
+    g = O.golden(B, Hq, Hkv, S, D, True, scale=GC.DEFAULT_SCALE, kind="pattern")
+    for ours, theirs in (("q", "q.f16"), ("k", "k.f16"), ("v", "v.f16"), ("dout", "dout.f16")):
+        np.testing.assert_array_equal(g[ours].view(np.uint16), a[theirs].view(np.uint16))
+    ulp = np.abs(g["out"].view(np.int16).astype(np.int32) - a["o.f16"].view(np.int16).astype(np.int32))
+    assert ulp.max() <= 1
+    np.testing.assert_allclose(g["scores_max"], a["scores_max.f32"], rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(g["scores_sum"], a["scores_sum.f32"], rtol=1e-5)
+    for n in ("delta", "dq", "dk", "dv"):
+        m = O.metrics(g[n], a[n + ".f32"])
+        ok, ref_ok = O.gates(n, m)
+        assert ok and ref_ok, (n, m)

@@ -95,3 +95,19 @@ def test_component_chain_from_golden_cache(tmp_path):
     pk = packed.cpu().numpy().reshape(1, 2, 512, 3)
     np.testing.assert_allclose(pk[..., :2], a["packed_sidecar.f32"][..., :2], rtol=1e-6)
     np.testing.assert_allclose(pk[..., 2], a["packed_sidecar.f32"][..., 2], rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("hq,hkv", [(1, 1), (4, 2)])
+def test_v2_on_reference_tool_cache(hq, hkv):
+    """v2 on the inputs of a cache written by the reference's own tool
+    (fixtures under tests/golden/reference_caches, made by
+    tests/golden/make_reference_caches.py), against that tool's fp32
+    gradients, under the reference's gates and the north-star bar."""
+    log(f"[case] reference tool cache v2 Hq{hq} Hkv{hkv} S128")
+    dims = dict(batch=1, heads_q=hq, heads_kv=hkv, seqlen=128, head_dim=128)
+    path = os.path.join(HERE, "golden", "reference_caches", GC.cache_key(causal=1, **dims))
+    g = as_golden(GC.read(path, causal=1, **dims), 1, GC.DEFAULT_SCALE)
+    res = run_v2(g, torch)
+    assert res["status"] == F.SUCCESS
+    rep = check(res, g, reference_gates=True)
+    log({n: round(m["max_rel"], 6) for n, m in rep.items()})
