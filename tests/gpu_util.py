@@ -70,8 +70,11 @@ def run_v2(g, torch, *, deterministic=False, with_softmax_d=True, lse=None, scal
 
 
 # bf16 has 8 significand bits against fp16's 11: P and dS, rounded to the
-# MFMA operand type, carry 8x the rounding error, so its bar is wider.
-BF16_GRAD_MAX_REL = 4e-2
+# MFMA operand type, carry 8x the rounding error, so its bar is wider: about
+# twice the worst max|err|/max|ref| measured over the bf16 cases of these
+# tests (5.4e-3, dQ at B1 H4 S2048 D128 causal).  The reference has no bf16
+# path, so this bar is this build's own (parity unpinned against it).
+BF16_GRAD_MAX_REL = 1.2e-2
 
 
 def check(res, g, names=("delta", "dq", "dk", "dv"), sel=None, reference_gates=False):
@@ -85,6 +88,7 @@ def check(res, g, names=("delta", "dq", "dk", "dv"), sel=None, reference_gates=F
         ok_ns, ok_ref = O.gates(n, m)
         if g.get("dtype", "fp16") == "bf16" and n != "delta":
             ok_ns = m["max_rel"] <= BF16_GRAD_MAX_REL and m["nonfinite"] == 0
+            log(f"bf16 {n} max_rel {m['max_rel']:.6f} (bar {BF16_GRAD_MAX_REL})")
         report[n] = m
         assert ok_ns, f"{n} fails max|err|/max|ref| bar: {m}"
         if reference_gates:
