@@ -131,9 +131,4 @@ __device__ __forceinline__ uint32_t tile_off(int row, int chunk) {
     return (uint32_t)(row * (D * 2) + ((chunk ^ sw) & (kChunks - 1)) * 16);
 }
 
-// dS^T tile [keys][64 queries] fp16: 8 chunks of 16 B per key row.
-__device__ __forceinline__ uint32_t dst_off(int key, int chunk) {
-    return (uint32_t)(key * 128 + ((chunk ^ swz128(key)) & 7) * 16);
-}
-
 }  // namespace fa3

@@ -197,7 +197,14 @@ __device__ __forceinline__ _Float16 to16(float x) {
 // loader `ld` moves the 16-byte chunk that belongs at LDS byte
 // blk * 1024 + lane * 16 (blk = ld * N + j); its source byte offset within the
 // global tile is precomputed once.
-template <int D, int N = Cfg<D>::kLoadsPerTile>
+// Row order of the tiles the score waves hold as B operands (the dKV job's
+// K / V, the dQ job's Q / dO): LDS row 16 b + i holds sequence row b + 4 i of
+// the tile, so score block b's 16 columns are rows b, b + 4, .., b + 60 (the
+// order that makes their P / dS stores conflict-free, see pds_off4).
+__device__ __forceinline__ int perm_row(int r) { return (r >> 4) + 4 * (r & 15); }
+
+// kPerm: LDS row r receives source row perm_row(r).
+template <int D, int N = Cfg<D>::kLoadsPerTile, bool kPerm = false>
 __device__ __forceinline__ void tile_load_offsets(uint32_t (&off)[N], int ld, int lane,
                                                   int row_stride) {
     using C = Cfg<D>;
@@ -210,7 +217,8 @@ __device__ __forceinline__ void tile_load_offsets(uint32_t (&off)[N], int ld, in
         if constexpr (C::kChunks == 16) sw = ((row & 3) << 2) | ((row >> 2) & 3);
         else sw = swz128(row);
         const int logical = (phys ^ sw) & (C::kChunks - 1);
-        off[j] = (uint32_t)((row * row_stride + logical * 8) * 2);
+        const int src = kPerm ? perm_row(row) : row;
+        off[j] = (uint32_t)((src * row_stride + logical * 8) * 2);
     }
 }
 
@@ -293,22 +301,49 @@ __device__ __forceinline__ void set_prio() {
 // A operand (32 x 16: m = D column, k = tile row) of a phase-2 product, read
 // transposed from a swizzled [64][D] tile: lane l gets column 32 db + l % 32,
 // rows 16 ks + 8 (l / 32) + t, t = 0..7 (two reads of 4 rows).
+// swap (wave-uniform): rows 16 ks + 8 (l / 32) + 4 .. + 7 first, then + 0 ..
+// + 3 -- the operand's two halves exchanged (see pds_off4).
 template <int D>
-__device__ __forceinline__ f16x8 tile_read_t(const FA3_LDS char* tile, int db, int ks, int lane) {
+__device__ __forceinline__ f16x8 tile_read_t(const FA3_LDS char* tile, int db, int ks, int lane,
+                                             bool swap = false) {
     const int g = lane >> 4, r = lane & 15;
     const int col = 32 * db + 16 * (g & 1) + 4 * (r & 3);
     const int row = 16 * ks + 8 * (g >> 1) + (r >> 2);
     const uint32_t lo = tile_off<D>(row, col >> 3) + (col & 7) * 2;
     const uint32_t hi = tile_off<D>(row + 4, col >> 3) + (col & 7) * 2;
-    return concat4(lds_read_tr4(tile, lo), lds_read_tr4(tile, hi));
+    return concat4(lds_read_tr4(tile, swap ? hi : lo), lds_read_tr4(tile, swap ? lo : hi));
 }
 
-// Byte offset of the 8-byte group (row r, columns 4 q .. 4 q + 3) of a
-// swizzled [64][64] fp16 P / dS tile.
+// P / dS tile [64 rows][64 columns], 16-bit, 8 chunks of 16 B (8 columns) per
+// row: P^T / dS^T of the dKV job (rows = keys, columns = query rows), dS of
+// the dQ job (rows = query rows, columns = keys).  Chunk c of row r sits at
+// r * 128 + (c ^ pds_swz(r)) * 16, its two 8-byte halves exchanged when r >=
+// 32.  A score wave stores 4 columns (8 B) of rows b + 4 i, i = lane % 16
+// (perm_row): pds_swz is a bijection on those rows' bits 2..4 and bit 5 picks
+// the half, so the 16 lanes a ds_write_b64 serves together (16 k .. 16 k + 15,
+// one 128-byte bank period) hit 16 distinct 8-byte slots.  The gradient waves'
+// ds_read_b128 of rows 32 blk + l % 32 (served in groups of 16 lanes chosen by
+// lane bit 5 and the parity of lane bits 2..4) stay conflict-free too; for
+// blk = 1 the operand holds its two 4-column halves exchanged, and the A
+// operand of the same product is exchanged to match (swap_halves, or
+// tile_read_t's swap).
+__device__ __forceinline__ int pds_swz(int r) { return ((r >> 2) & 7) ^ ((r >> 1) & 1); }
+__device__ __forceinline__ uint32_t pds_chunk(int r, int c) {
+    return (uint32_t)(r * 128 + ((c ^ pds_swz(r)) & 7) * 16);
+}
+// byte offset of columns 4 q .. 4 q + 3 of row r
 __device__ __forceinline__ uint32_t pds_off4(int r, int q) {
-    return dst_off(r, q >> 1) + (q & 1) * 8;
+    return pds_chunk(r, q >> 1) + (((q & 1) ^ (r >> 5)) & 1) * 8;
 }
-
+// (two 64-bit register moves)
+__device__ __forceinline__ f16x8 swap_halves(f16x8 x) {
+    typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+    const u64x2 v = __builtin_bit_cast(u64x2, x);
+    unsigned long long lo, hi;
+    __asm__("v_mov_b64 %0, %1" : "=v"(lo) : "v"(v[1]));
+    __asm__("v_mov_b64 %0, %1" : "=v"(hi) : "v"(v[0]));
+    return __builtin_bit_cast(f16x8, u64x2{lo, hi});
+}
 // Element offset of sequence row s of head h in batch b.
 template <int D>
 __device__ __forceinline__ size_t q_elem(const FusedArgs& a, int b, int h, int s) {
@@ -345,12 +380,34 @@ __device__ __forceinline__ int dkv_pair(int t, int u) {
     return 2 * ((D / 64) * (t & 1) + u) + (t >> 1);
 }
 
-// Byte offset of 16-byte chunk c (of 4) of row r in a [rows][32] fp16
-// staging tile (64-byte rows, chunks XOR-swizzled by r / 4): 16 rows x 4
-// chunks read with ds_read_b128 and 32 rows x 8 bytes written with
-// ds_write_b64 are both bank-conflict free.
-__device__ __forceinline__ uint32_t row64_off(int r, int c) {
-    return (uint32_t)(r * 64 + ((c ^ (r >> 2)) & 3) * 16);
+// Output staging tiles of the epilogues, 16-bit, [rows][32] (64-byte rows,
+// 4 chunks of 16 B) or [rows][64] (128-byte rows, 8 chunks): byte offset of
+// half `hf` (8 bytes) of chunk c of row r.  A gradient wave writes one half
+// of one chunk for 16 consecutive rows per ds_write_b64 lane group (one
+// 128-byte bank period): the chunk XOR (row bits 1..2, or 0..2) and the half
+// flip (row bit 3) put those 16 writes on distinct 8-byte slots.  The
+// read-back (ds_read_b128 of whole chunks, rows with bit 3 uniform per
+// instruction) stays conflict-free and swaps the halves of rows with bit 3
+// set back (stage_fix).
+__device__ __forceinline__ uint32_t stage64_chunk(int r, int c) {  // 16-byte aligned
+    return (uint32_t)(r * 64 + ((c ^ (r >> 1)) & 3) * 16);
+}
+__device__ __forceinline__ uint32_t stage128_chunk(int r, int c) {  // 16-byte aligned
+    return (uint32_t)(r * 128 + ((c ^ r) & 7) * 16);
+}
+__device__ __forceinline__ uint32_t stage64_off(int r, int c, int hf) {
+    return stage64_chunk(r, c) + ((hf ^ (r >> 3)) & 1) * 8;
+}
+__device__ __forceinline__ uint32_t stage128_off(int r, int c, int hf) {
+    return stage128_chunk(r, c) + ((hf ^ (r >> 3)) & 1) * 8;
+}
+__device__ __forceinline__ f16x8 stage_fix(f16x8 x, int r) {
+    return (r & 8) ? __builtin_shufflevector(x, x, 4, 5, 6, 7, 0, 1, 2, 3) : x;
+}
+// Row of read-back instruction j, lane `lane`, of a 64-byte-row staging
+// tile: lanes 4 i .. 4 i + 3 read the 4 chunks of one row; row bit 3 = j & 1.
+__device__ __forceinline__ int stage64_row(int j, int lane) {
+    return ((lane >> 2) & 7) | ((j & 1) << 3) | (((lane >> 5) & 1) << 4) | ((j >> 1) << 5);
 }
 
 // dV^T / dK^T accumulators of gradient wave t (pairs dkv_pair(t, u)) to dV /
@@ -381,8 +438,9 @@ __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[e] = to16<kBf16>(acc[u][kb][4 * a4 + e] * mul);
                     const int key = 32 * kb + l32;
-                    const uint32_t off = D == 128 ? dst_off(key, 4 * u + a4) : row64_off(key, a4);
-                    lds_write_b64(st, off + 8 * h, v);
+                    const uint32_t off =
+                        D == 128 ? stage128_off(key, 4 * u + a4, h) : stage64_off(key, a4, h);
+                    lds_write_b64(st, off, v);
                 }
         // the wave reads back only what it wrote: its LDS accesses complete in order
 #pragma unroll
@@ -392,10 +450,11 @@ __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase
                 key = 8 * j + ((lane >> 2) & 7);
                 c = (lane & 3) | ((lane >> 5) << 2);
             } else {
-                key = 16 * j + (lane >> 2);
+                key = stage64_row(j, lane);
                 c = lane & 3;
             }
-            const f16x8 x = lds_read_b128(st, D == 128 ? dst_off(key, c) : row64_off(key, c));
+            const f16x8 x = stage_fix(
+                lds_read_b128(st, D == 128 ? stage128_chunk(key, c) : stage64_chunk(key, c)), key);
             *(f16x8*)(outp + base + (size_t)key * a.kv_rs + d0 + 8 * c) = x;
         }
         return;
@@ -439,13 +498,13 @@ __device__ __forceinline__ void store_dq(const FusedArgs& a, size_t base, int t,
                 f16x4 v;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = to16<kBf16>(acc[r][4 * a4 + e] * a.scale);
-                lds_write_b64(st, row64_off(32 * r + l32, a4) + 8 * h, v);
+                lds_write_b64(st, stage64_off(32 * r + l32, a4, h), v);
             }
         _Float16* outp = (_Float16*)a.dq + base + 32 * db;
 #pragma unroll
         for (int j = 0; j < 2 * kRb; ++j) {
-            const int r = 16 * j + (lane >> 2), c = lane & 3;  // r: row within the wave's block
-            const f16x8 x = lds_read_b128(st, row64_off(r, c));
+            const int r = stage64_row(j, lane), c = lane & 3;  // r: row within the wave's block
+            const f16x8 x = stage_fix(lds_read_b128(st, stage64_chunk(r, c)), r);
             *(f16x8*)(outp + (size_t)(32 * rb0 + r) * a.q_rs + 8 * c) = x;
         }
         return;
@@ -618,7 +677,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
     const bool loads = !C::kGradLoads || w >= 4;
     uint32_t ld_off[C::kNld], kv_off[C::kLoadsPerTile];
     tile_load_offsets<D, C::kNld>(ld_off, ldr, lane, a.q_rs);
-    tile_load_offsets<D>(kv_off, w, lane, a.kv_rs);
+    tile_load_offsets<D, C::kLoadsPerTile, true>(kv_off, w, lane, a.kv_rs);
 
     // Cursor of the next query tile to load; a finished stream keeps
     // re-loading its last tile (into a stage nobody reads), so every step
@@ -690,10 +749,11 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
 
     if (w < 4) {
         // ---- score waves: S, dP, P, dS of query rows 16 t .. +16 and all 64
-        // keys (four 16-key blocks); P^T and dS^T go to LDS.
-        // B operands: key 16 kb + l16, D chunk p1_chunk(s, g4)
+        // keys (four 16-key blocks kb: keys kb + 4 l16, perm_row); P^T and
+        // dS^T go to LDS.
+        // B operands: LDS row 16 kb + l16 (key kb + 4 l16), D chunk p1_chunk(s, g4)
         f16x8 kf[4][C::kKs], vf[4][C::kKs];
-        f32x4 sacc[4], pacc[4];  // rows 16 t + 4 g4 + i, keys 16 kb + l16
+        f32x4 sacc[4], pacc[4];  // rows 16 t + 4 g4 + i, keys kb + 4 l16
         int sm_qt = qa;          // query tile of the next softmax
         auto next_masked = [&]() {
             const bool m = kCausal && sm_qt == kt;
@@ -755,7 +815,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                 __asm__ volatile("" ::: "memory");  // keep this a branch
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    if (16 * (e >> 2) + l16 > 16 * t + 4 * g4 + (e & 3)) {
+                    if ((e >> 2) + 4 * l16 > 16 * t + 4 * g4 + (e & 3)) {
                         p[e] = 0.f;
                         ds[e] = 0.f;
                     }
@@ -769,7 +829,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                     pv[i] = to16<kBf16>(p[4 * kb + i]);
                     dv[i] = to16<kBf16>(ds[4 * kb + i]);
                 }
-                const uint32_t off = pds_off4(16 * kb + l16, 4 * t + g4);
+                const uint32_t off = pds_off4(kb + 4 * l16, 4 * t + g4);
                 lds_write_b64(pds, off, pv);
                 lds_write_b64(pds + C::kPdsBytes, off, dv);
             }
@@ -848,16 +908,20 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
-                    bp[ks][kb] = lds_read_b128(m, dst_off(32 * kb + l32, 2 * ks + h));
+                    bp[ks][kb] = lds_read_b128(m, pds_chunk(32 * kb + l32, 2 * ks + h));
             __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
             set_prio<0>();  // raised for the step's LDS reads (see step)
+            // key block 1's operands arrive with their halves exchanged
+            // (pds_off4): its products take the A operands exchanged too,
+            // copied while block 0's products run
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-                for (int u = 0; u < kPpw; ++u)
+                for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-                        acc[u][kb] = mfma_32x32x16t<kBf16>(xt[u][ks], bp[ks][kb], acc[u][kb]);
+                    for (int u = 0; u < kPpw; ++u)
+                        acc[u][kb] = mfma_32x32x16t<kBf16>(kb ? swap_halves(xt[u][ks]) : xt[u][ks],
+                                                           bp[ks][kb], acc[u][kb]);
         };
         auto prologue = [&](const FA3_LDS char* __restrict__ s0) {
             wait_vm_lgkm0<2 * C::kDmaKv>();  // the first tile has landed
@@ -948,7 +1012,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
     const bool loads = !C::kGradLoads || w >= 4;
     uint32_t ld_off[C::kNld], q_off[C::kLoadsPerTile];
     tile_load_offsets<D, C::kNld>(ld_off, ldr, lane, a.kv_rs);
-    tile_load_offsets<D>(q_off, w, lane, a.q_rs);
+    tile_load_offsets<D, C::kLoadsPerTile, true>(q_off, w, lane, a.q_rs);
     const _Float16* kh = a.k + kv_elem<D>(a, b, hkv, 0);
     const _Float16* vh = a.v + kv_elem<D>(a, b, hkv, 0);
     int ld_kt = ka;
@@ -999,12 +1063,13 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
 
     if (w < 4) {
         // ---- score waves: S^T, dP^T, dS^T of keys 16 t .. +16 of each key
-        // tile and all 64 query rows (four 16-row blocks); dS goes to LDS.
-        // B operands: row 16 rb + l16, D chunk p1_chunk(s, g4)
+        // tile and all 64 query rows (four 16-row blocks rb: rows rb + 4 l16,
+        // perm_row); dS goes to LDS.
+        // B operands: LDS row 16 rb + l16 (query row rb + 4 l16), D chunk p1_chunk(s, g4)
         f16x8 qf[4][C::kKs], df[4][C::kKs];
         float l2[4];
-        f32x4 ndl[4];            // -delta of row 16 rb + l16, the dP^T accumulators' start
-        f32x4 sacc[4], pacc[4];  // keys 16 t + 4 g4 + i, rows 16 rb + l16
+        f32x4 ndl[4];            // -delta of row rb + 4 l16, the dP^T accumulators' start
+        f32x4 sacc[4], pacc[4];  // keys 16 t + 4 g4 + i, rows rb + 4 l16
         auto score = [&](bool masked, const FA3_LDS char* st, FA3_LDS char* ds) {
             f16x8 ak[C::kKs], av[C::kKs];
             set_prio<3>();
@@ -1034,24 +1099,24 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
                 __asm__ volatile("" ::: "memory");  // keep this a branch
 #pragma unroll
                 for (int e = 0; e < 16; ++e)
-                    if (16 * t + 4 * g4 + (e & 3) > 16 * (e >> 2) + l16) p[e] = 0.f;
+                    if (16 * t + 4 * g4 + (e & 3) > (e >> 2) + 4 * l16) p[e] = 0.f;
             }
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
                 f16x4 dv;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) dv[i] = to16<kBf16>(p[4 * rb + i]);
-                lds_write_b64(ds, pds_off4(16 * rb + l16, 4 * t + g4), dv);
+                lds_write_b64(ds, pds_off4(rb + 4 * l16, 4 * t + g4), dv);
             }
         };
         auto prologue = [&](FA3_LDS char* __restrict__ s0, FA3_LDS char* __restrict__ pa) {
             const FA3_LDS float* rows = (const FA3_LDS float*)(s0 + 2 * C::kTileBytes);
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
-                const int r = 16 * rb + l16;
+                const int r = rb + 4 * l16;  // query row, held at LDS row 16 rb + l16
 #pragma unroll
                 for (int s = 0; s < C::kKs; ++s) {
-                    const uint32_t off = tile_off<D>(r, p1_chunk<D>(s, g4));
+                    const uint32_t off = tile_off<D>(16 * rb + l16, p1_chunk<D>(s, g4));
                     qf[rb][s] = lds_read_b128(pa, off);
                     df[rb][s] = lds_read_b128(pa + C::kTileBytes, off);
                 }
@@ -1104,9 +1169,13 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
 #pragma unroll
         for (int r = 0; r < kRb; ++r) acc[r] = f32x16{};
         f16x8 xa[4], xb[4];  // K^T of a key tile, per k-step
+        // row block 1's dS operands arrive with their halves exchanged
+        // (pds_off4): at D 64 the wave's only block is rb0 and its K^T
+        // operands are read exchanged; at D 128 block 1 takes swap_halves
+        const bool swap_read = kRb == 1 && rb0 == 1;
         auto read_xt = [&](const FA3_LDS char* st, f16x8 (&xt)[4]) {
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) xt[ks] = tile_read_t<D>(st, db, ks, lane);
+            for (int ks = 0; ks < 4; ++ks) xt[ks] = tile_read_t<D>(st, db, ks, lane, swap_read);
         };
         auto grad = [&](const f16x8 (&xt)[4], const FA3_LDS char* ds) {
             f16x8 bd[4][kRb];  // all B operands first: one LDS round trip
@@ -1114,13 +1183,15 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
                 for (int r = 0; r < kRb; ++r)
-                    bd[ks][r] = lds_read_b128(ds, dst_off(32 * (rb0 + r) + l32, 2 * ks + h));
+                    bd[ks][r] = lds_read_b128(ds, pds_chunk(32 * (rb0 + r) + l32, 2 * ks + h));
             __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
             set_prio<0>();  // as in dkv_role
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-                for (int r = 0; r < kRb; ++r) acc[r] = mfma_32x32x16t<kBf16>(xt[ks], bd[ks][r], acc[r]);
+                for (int r = 0; r < kRb; ++r)
+                    acc[r] = mfma_32x32x16t<kBf16>(kRb == 2 && r == 1 ? swap_halves(xt[ks]) : xt[ks],
+                                                   bd[ks][r], acc[r]);
         };
         auto prologue = [&](const FA3_LDS char* __restrict__ s0) {
             wait_vm_lgkm0<2 * C::kDmaQ>();
