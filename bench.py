@@ -4,13 +4,14 @@ A step is one full backward through the C ABI over resident fp16 inputs at
 the headline shape B=1, H=4, S=2048, D=128, causal (BASELINE.json
 configs[2]): the delta preprocess and the main kernel, two launches on the
 null stream.  The timed region is `steps` back-to-back shaobo_fa3_bwd_v2
-calls between two HIP events.  A second run of as many back-to-back calls,
-through shaobo_fa3_ext_bwd_v2_timed (v2 that also records an event before,
-between and after the two kernels), gives each kernel's average duration in
-the same regime, from which the rooflines are computed.  Each event marker
-delays the next kernel's start by its dispatch latency, which the interval
-then includes, so these per-kernel durations (and the rooflines drawn from
-them) are upper bounds on the pure execution times a kernel trace reports.  Prints one JSON
+calls between two HIP events.  Per-kernel durations, back to back: the
+preprocess kernel alone (the same kernel and grid through the
+shaobo_fa3_bwd_dot_do_o component) over as many back-to-back launches
+between two events, and the main kernel as the step minus that; the
+rooflines come from these.  For reference the line also carries the
+durations measured by shaobo_fa3_ext_bwd_v2_timed (events recorded before,
+between and after the two kernels of every call), which include each
+marker's dispatch latency and so exceed the kernels' execution times.  Prints one JSON
 line: TFLOP/s from FLOPs = 10*B*H*S^2*D*0.5, ms per backward, % of fp16 dense
 MFMA peak, the main kernel's (MFMA) and the preprocess's (HBM) rooflines,
 and the CPU oracle timed on the host as the reported CPU baseline.
@@ -240,8 +241,32 @@ def main():
     f = flops(B, Hq, S, D, causal)
     tflops = f / (ms * 1e-3) / 1e12
 
-    # ---- per-kernel durations, back to back: the same number of calls
-    # through the timed entry, three events per call, read after one sync ----
+    # ---- per-kernel durations, back to back ----
+    # the preprocess alone: the dot_do_o component runs the same kernel on
+    # the same rows (delta plus the packed sidecar: the same bytes)
+    pp = F.make_params(lib, batch=B, seqlen=S, heads_q=Hq, heads_kv=Hq, head_dim=D,
+                       causal=causal, softmax_scale=scale)
+    pp.softmax_aux_mode = F.AUX_LSE
+    packed = torch.empty(B * Hq * S * 3, dtype=torch.float32, device="cuda")
+
+    def pre_step():
+        st = lib.shaobo_fa3_bwd_dot_do_o(c(do), c(out), c(lse), None, c(delta), c(packed),
+                                         ctypes.byref(pp))
+        if st != F.SUCCESS:
+            raise RuntimeError("shaobo_fa3_bwd_dot_do_o: " + F.status_name(st))
+
+    for _ in range(20):
+        pre_step()
+    torch.cuda.synchronize()
+    hip.record(e0)
+    for _ in range(args.steps):
+        pre_step()
+    hip.record(e1)
+    torch.cuda.synchronize()
+    pre_ms = hip.elapsed_ms(e0, e1) / args.steps
+    main_ms = ms - pre_ms
+    # the same number of calls through the timed entry, three events per
+    # call, read after one sync (marker-inclusive durations)
     evs = [[hip.event() for _ in range(3)] for _ in range(args.steps)]
     ev_arrays = [(ctypes.c_void_p * 3)(*[e.value for e in trio]) for trio in evs]
     for i in range(args.steps):
@@ -249,8 +274,8 @@ def main():
         if st != F.SUCCESS:
             raise RuntimeError("shaobo_fa3_ext_bwd_v2_timed: " + F.status_name(st))
     torch.cuda.synchronize()
-    pre_ms = sum(hip.elapsed_ms(t[0], t[1]) for t in evs) / args.steps
-    main_ms = sum(hip.elapsed_ms(t[1], t[2]) for t in evs) / args.steps
+    pre_marked = sum(hip.elapsed_ms(t[0], t[1]) for t in evs) / args.steps
+    main_marked = sum(hip.elapsed_ms(t[1], t[2]) for t in evs) / args.steps
     staged_ms = hip.elapsed_ms(evs[0][0], evs[-1][2]) / args.steps
     main_tflops = f / (main_ms * 1e-3) / 1e12
     pre_gbs = preprocess_bytes(B, Hq, S, D) / (pre_ms * 1e-3) / 1e9
@@ -278,7 +303,9 @@ def main():
         "warmup_steps_run": done,
         "warmup_s": round(warm_s, 3),
         "kernels_ms": {"preprocess_kernel": round(pre_ms, 5), "bwd_main_kernel": round(main_ms, 5)},
-        "staged_ms_per_step": round(staged_ms, 5),
+        "kernels_ms_marked": {"preprocess_kernel": round(pre_marked, 5),
+                              "bwd_main_kernel": round(main_marked, 5),
+                              "ms_per_step": round(staged_ms, 5)},
         "roofline": {"kernel": "bwd_main_kernel", "bound": "mfma",
                      "achieved": round(main_tflops, 3),
                      "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
