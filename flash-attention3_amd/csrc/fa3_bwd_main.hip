@@ -653,7 +653,7 @@ __device__ __forceinline__ bool split_end(const A& a, int job, FA3_LDS int* flag
 // Streams query tiles [qa, qb) of every query head of the group.  slot < 0:
 // the job is whole and writes dK / dV; otherwise the unit is piece slot & 1
 // of split job slot >> 1 and the pieces' partial sums meet in split_end.
-template <int D, bool kCausal, bool kBf16, int kRows = 0>
+template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false>
 __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, int slot,
                          FA3_LDS char* smem) {
     static_assert(kRows == 0 || kRows == 1, "dKV rows come as lse2/-delta or packed");
@@ -762,7 +762,8 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         };
         // S = Q K^T and dP - delta = dO V^T - delta, then P and dS, written
         // transposed ([key][row]) into the P / dS buffer
-        auto score = [&](bool masked, const FA3_LDS char* st, FA3_LDS char* pds) {
+        auto score = [&](bool masked, const FA3_LDS char* st, FA3_LDS char* pds,
+                         FA3_LDS char* ld, bool do_issue) {
             f16x8 aq[C::kKs], ad[C::kKs];
             set_prio<3>();
 #pragma unroll
@@ -793,7 +794,13 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                 }
             }
             // all operand reads in flight before the first MFMA: the waits
-            // then count down instead of draining the LDS queue per k-step
+            // then count down instead of draining the LDS queue per k-step.
+            // kLateIssue (split plan): this wave's loads of the tile after
+            // next go out behind them (P3 -1 %); otherwise right after the
+            // barrier (step), which suits the default plan's longer loads
+            // (more L2 misses; P4 +0.6 % the other way)
+            __builtin_amdgcn_sched_barrier(0);
+            if (!C::kGradLoads && kLateIssue && do_issue) issue(ld);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int s = 0; s < C::kKs; ++s) {
@@ -849,14 +856,14 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
             if constexpr (C::kGradLoads) wait_vm_lgkm0<0>();  // K / V reads done before P / dS overwrite them
             else wait_vm_lgkm0<2 * C::kDmaKv>();
             barrier();
-            score(next_masked(), s0, pa);
+            score(next_masked(), s0, pa, pa, false);
         };
         auto step = [&](FA3_LDS char* __restrict__ ld, const FA3_LDS char* __restrict__ s1,
                         FA3_LDS char* __restrict__ pwr) {
             top();
-            if constexpr (!C::kGradLoads) issue(ld);
+            if constexpr (!C::kGradLoads && !kLateIssue) issue(ld);
             __builtin_amdgcn_sched_barrier(0);
-            score(next_masked(), s1, pwr);
+            score(next_masked(), s1, pwr, ld, true);
             __builtin_amdgcn_sched_barrier(0);
         };
         prologue_loads();
@@ -987,7 +994,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
 // ----------------------------------------------------------------------------
 // Streams key tiles [ka, kb) (the causal diagonal, key tile qt, is masked).
 // slot: as for dkv_role.
-template <int D, bool kCausal, bool kBf16, int kRows = 0>
+template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false>
 __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int slot,
                         FA3_LDS char* smem) {
     static_assert(kRows == 0 || kRows == 2, "dQ rows come as lse2/-delta or max/sum/delta");
@@ -1070,7 +1077,8 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         float l2[4];
         f32x4 ndl[4];            // -delta of row rb + 4 l16, the dP^T accumulators' start
         f32x4 sacc[4], pacc[4];  // keys 16 t + 4 g4 + i, rows rb + 4 l16
-        auto score = [&](bool masked, const FA3_LDS char* st, FA3_LDS char* ds) {
+        auto score = [&](bool masked, const FA3_LDS char* st, FA3_LDS char* ds,
+                         FA3_LDS char* ld, bool do_issue) {
             f16x8 ak[C::kKs], av[C::kKs];
             set_prio<3>();
 #pragma unroll
@@ -1080,6 +1088,8 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
                 av[s] = lds_read_b128(st + C::kTileBytes, off);
             }
             __builtin_amdgcn_sched_barrier(0);  // as in dkv_role
+            if (!C::kGradLoads && kLateIssue && do_issue) issue(ld);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int s = 0; s < C::kKs; ++s) {
 #pragma unroll
@@ -1133,15 +1143,15 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
             if constexpr (C::kGradLoads) wait_vm_lgkm0<0>();  // Q / dO reads done before dS overwrites them
             else wait_vm_lgkm0<2 * C::kDmaQ>();
             barrier();
-            score(kCausal && ka == qt, s0, pa);
+            score(kCausal && ka == qt, s0, pa, pa, false);
         };
         // step j computes the dS of key tile ka + j + 1
         auto step = [&](bool masked, FA3_LDS char* __restrict__ ld,
                         const FA3_LDS char* __restrict__ s1, FA3_LDS char* __restrict__ pwr) {
             top();
-            if constexpr (!C::kGradLoads) issue(ld);
+            if constexpr (!C::kGradLoads && !kLateIssue) issue(ld);
             __builtin_amdgcn_sched_barrier(0);
-            score(masked, s1, pwr);
+            score(masked, s1, pwr, ld, true);
             __builtin_amdgcn_sched_barrier(0);
         };
         prologue_loads();
@@ -1286,45 +1296,49 @@ __device__ __forceinline__ void job_of(const FusedArgs& a, int& g, int& pos) {
 // The host picks the head lengths from a cost model of the steps, prologues
 // and epilogues so that the workgroups finish together (a length covering
 // the whole job leaves it unsplit).
-template <int D, bool kCausal, bool kBf16>
+//
+// kSplit selects the split plan (a separate instantiation: its units issue
+// their loads at a different point of the step, see dkv_role's score).
+template <int D, bool kCausal, bool kBf16, bool kSplit>
 __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
+    static_assert(kCausal || !kSplit, "the split plan is causal");
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
     int g, pos;
     job_of(a, g, pos);
     const int group = a.heads_q / a.heads_kv;
     const int QT = a.seqlen / 64;
-    if (kCausal && a.bal_m > 0) {
+    if constexpr (kSplit) {
         // G = 1: group g is query head g (and KV head g)
         const int M = a.bal_m;
         const int job0 = g * M;
         if (pos < M) {
             // dKV key tile M + x whole, then the remainder of dQ query tile M + x
             const int x = pos, nq = M + x + 1, lq = a.head_q[x];
-            dkv_role<D, kCausal, kBf16>(a, g, M + x, M + x, QT, -1, smem);
+            dkv_role<D, kCausal, kBf16, 0, true>(a, g, M + x, M + x, QT, -1, smem);
             if (lq < nq) {
                 wait_vm_lgkm0<0>();
                 barrier();
-                dq_role<D, kCausal, kBf16>(a, g, M + x, lq, nq, 2 * (job0 + x) + 1, smem);
+                dq_role<D, kCausal, kBf16, 0, true>(a, g, M + x, lq, nq, 2 * (job0 + x) + 1, smem);
             }
         } else if (pos < 2 * M) {
             // dQ query tile x whole, then the remainder of dKV key tile x
             const int x = pos - M, nkv = QT - x, lkv = a.head_kv[x];
-            dq_role<D, kCausal, kBf16>(a, g, x, 0, x + 1, -1, smem);
+            dq_role<D, kCausal, kBf16, 0, true>(a, g, x, 0, x + 1, -1, smem);
             if (lkv < nkv) {
                 wait_vm_lgkm0<0>();
                 barrier();
-                dkv_role<D, kCausal, kBf16>(a, g, x, x + lkv, QT, 2 * (job0 + x) + 1, smem);
+                dkv_role<D, kCausal, kBf16, 0, true>(a, g, x, x + lkv, QT, 2 * (job0 + x) + 1, smem);
             }
         } else if (pos < 3 * M) {
             // head piece (or all) of dKV key tile x
             const int x = pos - 2 * M, nkv = QT - x, lkv = a.head_kv[x];
-            dkv_role<D, kCausal, kBf16>(a, g, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1,
+            dkv_role<D, kCausal, kBf16, 0, true>(a, g, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1,
                                  smem);
         } else {
             // head piece (or all) of dQ query tile M + x
             const int x = pos - 3 * M, nq = M + x + 1, lq = a.head_q[x];
-            dq_role<D, kCausal, kBf16>(a, g, M + x, 0, min(lq, nq), lq < nq ? 2 * (job0 + x) : -1, smem);
+            dq_role<D, kCausal, kBf16, 0, true>(a, g, M + x, 0, min(lq, nq), lq < nq ? 2 * (job0 + x) : -1, smem);
         }
         return;
     }
@@ -1362,12 +1376,16 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_component_kernel(FusedArgs a)
 template <int D>
 void launch_d(const FusedArgs& a, bool causal, bool bf16, hipStream_t stream) {
     const dim3 grid(a.n_groups * a.jobs_per_group);
+    const dim3 block(kThreads);
+    const bool split = a.bal_m > 0;  // causal only (plan_workspace)
     if (bf16) {
-        if (causal) hipLaunchKernelGGL((bwd_main_kernel<D, true, true>), grid, dim3(kThreads), 0, stream, a);
-        else hipLaunchKernelGGL((bwd_main_kernel<D, false, true>), grid, dim3(kThreads), 0, stream, a);
+        if (split) hipLaunchKernelGGL((bwd_main_kernel<D, true, true, true>), grid, block, 0, stream, a);
+        else if (causal) hipLaunchKernelGGL((bwd_main_kernel<D, true, true, false>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((bwd_main_kernel<D, false, true, false>), grid, block, 0, stream, a);
     } else {
-        if (causal) hipLaunchKernelGGL((bwd_main_kernel<D, true, false>), grid, dim3(kThreads), 0, stream, a);
-        else hipLaunchKernelGGL((bwd_main_kernel<D, false, false>), grid, dim3(kThreads), 0, stream, a);
+        if (split) hipLaunchKernelGGL((bwd_main_kernel<D, true, false, true>), grid, block, 0, stream, a);
+        else if (causal) hipLaunchKernelGGL((bwd_main_kernel<D, true, false, false>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((bwd_main_kernel<D, false, false, false>), grid, block, 0, stream, a);
     }
 }
 
