@@ -577,21 +577,26 @@ __device__ __forceinline__ void add_partials(__amdgpu_buffer_rsrc_t r, uint32_t 
 // words once it has seen the ready word, so a replayed launch that reuses
 // its epoch (graph capture) finds them cleared too.
 //
-// split_arrive: thread 0 swaps the epoch into the arrival word.  The piece
-// that reads back the epoch arrived second; the other arrived first.
-// split_end (every wave, after its last pipeline step; the gradient
-// waves pass put_own storing their partial sums, the score waves a no-op):
-// the first piece stores its partial sums, waits until
-// its stores have completed (s_waitcnt vmcnt(0) covers stores on gfx9) and
-// writes the epoch into the ready word; it writes nothing else.  The second
-// piece waits for the ready word (one thread, a bounded spin) and then adds
-// the first piece's partial sums and writes the output.  The output is piece
-// 0 + piece 1 either way (a two-term fp32 sum is the same in either order),
-// so the result does not depend on which piece finishes first.  The wait
-// cannot block for long -- the first piece has left its loop and only
-// stores after arriving -- but it is bounded all the same; a wait that gives
-// up writes the epoch into the error word, which the host reports as a HIP
-// error when it synchronises, so a timed-out sum is never silent.
+// split_arrive (thread 0, right after the score waves' last barrier, while
+// the gradient waves run the last products): swaps the epoch into the arrival
+// word.  The piece that reads back the epoch arrived second; it then waits
+// for the ready word at once (a bounded spin), so that wait overlaps the
+// gradient waves' last products instead of following them, and clears both
+// words without waiting for those stores (nobody reads the words again in
+// this launch).  *flag: 0 first, 1 second.
+// split_end (every wave, after its last pipeline step; the gradient waves
+// pass put_own storing their partial sums, the score waves a no-op): the
+// first piece stores its partial sums, waits until its stores have
+// completed (s_waitcnt vmcnt(0) covers stores on gfx9) and writes the epoch
+// into the ready word; it writes nothing else.  The second piece, past the
+// barrier that follows its wait, adds the first piece's partial sums and
+// writes the output.  The output is piece 0 + piece 1 either way (a
+// two-term fp32 sum is the same in either order), so the result does not
+// depend on which piece finishes first.  The wait cannot block for long --
+// the first piece has left its loop and only stores after arriving -- but
+// it is bounded all the same; a wait that gives up writes the epoch into the
+// error word, which the host reports as a HIP error when it synchronises, so
+// a timed-out sum is never silent.
 //
 // Ordering: every cross-workgroup access (words and partial sums) is an
 // agent-scope access with the sc1 policy, coherent at the device level; the
@@ -603,48 +608,43 @@ __device__ __forceinline__ void split_arrive(const A& a, int job, FA3_LDS int* f
     if (threadIdx.x == 0) {
         const unsigned long long old = __hip_atomic_exchange(
             a.sync + 2 * job, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = old == a.epoch ? 1 : 0;
+        const bool second = old == a.epoch;
+        if (second) {
+            bool seen = false;
+            for (int i = 0; i < a.spin_limit; ++i) {
+                if (__hip_atomic_load(a.sync + 2 * job + 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == a.epoch) {
+                    seen = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (!seen)
+                __hip_atomic_store(a.err, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // leave the words cleared, so that a replay of the same launch (a
+            // captured graph keeps the epoch) starts from "nobody arrived"
+            __hip_atomic_store(a.sync + 2 * job, 0ull, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.sync + 2 * job + 1, 0ull, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        *flag = second ? 1 : 0;
     }
 }
 
 template <typename A, typename PutOwn>
 __device__ __forceinline__ bool split_end(const A& a, int job, FA3_LDS int* flag,
                                           PutOwn&& put_own) {
+    wait_vm_lgkm0<63>();  // lgkmcnt(0): the flag's LDS store is done
+    barrier();
+    if (*flag != 0) return true;
+    put_own();
     wait_vm_lgkm0<0>();
     barrier();
-    const int second = *flag;
-    if (!second) {
-        put_own();
-        wait_vm_lgkm0<0>();
-        barrier();
-        if (threadIdx.x == 0)
-            __hip_atomic_store(a.sync + 2 * job + 1, a.epoch, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        return false;
-    }
-    if (threadIdx.x == 0) {
-        bool seen = false;
-        for (int i = 0; i < a.spin_limit; ++i) {
-            if (__hip_atomic_load(a.sync + 2 * job + 1, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT) == a.epoch) {
-                seen = true;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        if (!seen)
-            __hip_atomic_store(a.err, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // Nobody reads the words again in this launch (the first piece wrote
-        // its last one before the ready word was seen): leave them cleared, so
-        // that a replay of the same launch (a captured graph keeps the epoch)
-        // starts from "nobody arrived".
-        __hip_atomic_store(a.sync + 2 * job, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.sync + 2 * job + 1, 0ull, __ATOMIC_RELAXED,
+    if (threadIdx.x == 0)
+        __hip_atomic_store(a.sync + 2 * job + 1, a.epoch, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
-    }
-    wait_vm_lgkm0<0>();
-    barrier();
-    return true;
+    return false;
 }
 
 // ----------------------------------------------------------------------------
