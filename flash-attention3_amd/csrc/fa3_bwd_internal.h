@@ -62,13 +62,13 @@ struct BwdTensors {
 // aligned):
 //   * the error word (one 64-bit word), set to the launch's epoch by a split
 //     wait that gives up;
-//   * lse2 and -delta rows, written by the preprocess pass;
+//   * -lse2 and -delta rows, written by the preprocess pass;
 //   * split plan only (bal_m > 0): two 64-bit synchronisation words per
 //     split job of each role, and the fp32 partial sums of one piece per
 //     split job (dKV jobs, then dQ jobs).
 struct WorkspacePlan {
     size_t err_off = 0;
-    size_t lse2_off = 0;
+    size_t nlse2_off = 0;
     size_t ndelta_off = 0;
     int bal_m = 0;          // > 0: split plan with M = bal_m
     int n_split = 0;        // split jobs per role
@@ -88,14 +88,15 @@ WorkspacePlan plan_workspace(const BwdProblem& p);
 hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace,
                            unsigned long long* epoch);
 
-// Delta preprocess: delta into t.delta, lse2 and -delta into the given rows;
+// Delta preprocess: delta into t.delta, -lse2 and -delta into the given rows;
 // any of the three may be null.  Alone, it is the component entry
 // shaobo_fa3_bwd_dot_do_o.
-hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
+hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* nlse2,
                              float* ndelta);
 
-// lse2 and -delta rows from the packed sidecar t.packed_in.
-hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta);
+// -lse2 and -delta rows from the packed sidecar t.packed_in.
+hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* nlse2,
+                           float* ndelta);
 
 // Workspace-free single-role components (causal, heads_q == heads_kv, fp32
 // outputs when p.out_f32): role 1 writes dK / dV from t.packed_in, role 2

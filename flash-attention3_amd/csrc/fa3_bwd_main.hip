@@ -3,8 +3,9 @@
 // src/fused_bwd_dq_reduce.cpp:27-109, and the legacy dKV / dQ kernels
 // src/dkv_kernel.cpp:957-1085, src/dq_kernel.cpp:794-953).  It runs after the
 // delta preprocess (fa3_bwd_preprocess.hip), which supplies per query row
-// lse2 = LSE * log2(e) and -delta = -rowsum(dO * O); the component kernels at
-// the end of this file read the reference's row statistics directly instead.
+// -lse2 = -LSE * log2(e) and -delta = -rowsum(dO * O); the component kernels
+// at the end of this file read the reference's row statistics directly
+// instead.
 //
 // Two job roles; each output element has one writer:
 //
@@ -17,7 +18,14 @@
 //    tiles it sees, recomputing S^T and dP^T, and accumulates dQ^T:
 //        S^T = K Q^T, dP^T = V dO^T, dS^T, dQ^T += K^T dS^T (3 GEMMs per tile)
 //
-// The softmax scale is folded out of dS and applied once to dK and dQ.
+// The softmax scale is folded out of dS and applied once to dK and dQ.  The
+// score waves' resident operand (K in the dKV role, Q in the dQ role) is
+// multiplied by c = scale * log2(e) in LDS as it lands (fp32 product,
+// rounded once to the operand type) and -lse2 seeds the S accumulators, so
+// the MFMAs leave S c - lse2 and P costs one exp2 per element (kScaled).
+// When c > 1 (scale > ln 2) K c or Q c could overflow fp16: those launches,
+// the split plan and the component kernels use the unscaled instantiations,
+// which apply c in the loop.
 //
 // A workgroup runs one job with 8 waves, two per SIMD, specialised:
 //   score waves 0..3: S and dP of 16 rows x 64 columns of the step's tile
@@ -65,10 +73,10 @@ struct FusedArgs {
     const _Float16* v;
     const _Float16* dout;
     // Row statistics, by row-source mode kRows of the role templates:
-    // 0: lse2 (= LSE log2 e) and -delta arrays written by a preprocess pass;
+    // 0: -lse2 (lse2 = LSE log2 e) and -delta arrays written by a preprocess pass;
     // 1: the packed sidecar [max_log2, inv_sum, delta] per row (dKV only);
     // 2: raw row max, row sum and delta arrays (dQ only).
-    const float* lse2;   // [B*Hq*S]
+    const float* nlse2;  // [B*Hq*S], -lse2
     const float* ndelta; // [B*Hq*S], -delta
     const float* packed; // [B*Hq*S][3]
     const float* smax;   // [B*Hq*S]
@@ -235,7 +243,7 @@ __device__ __forceinline__ void load_tile_async(FA3_LDS char* tile, const _Float
 // Direct-to-LDS copy of the statistics of the 64 query rows row0 .. of a
 // streamed tile by the 4 gradient waves, loader t moving rows 16 t .. 16 t +
 // 15 (one load each; one dword per active lane):
-//   kRows 0: lse2 -> rows[32 t .. 32 t + 16), -delta -> rows[32 t + 16 ..
+//   kRows 0: -lse2 -> rows[32 t .. 32 t + 16), -delta -> rows[32 t + 16 ..
 //            32 t + 32) (lanes 0..31);
 //   kRows 1: packed[3 (row0 + 16 t) ..] -> rows[48 t .. 48 t + 48), i.e. the
 //            [row][3] layout of all 64 rows (lanes 0..47).
@@ -243,7 +251,7 @@ template <int kRows>
 __device__ __forceinline__ void load_rows4_async(FA3_LDS char* rows, const FusedArgs& a,
                                                  size_t row0, int t, int lane) {
     if constexpr (kRows == 0) {
-        const float* src = (lane < 16 ? a.lse2 : a.ndelta) + row0 + 16 * t + (lane & 15);
+        const float* src = (lane < 16 ? a.nlse2 : a.ndelta) + row0 + 16 * t + (lane & 15);
         if (lane < 32)
             __builtin_amdgcn_global_load_lds((const void*)src, (FA3_LDS void*)(rows + 128 * t), 4,
                                              0, 0);
@@ -257,7 +265,7 @@ __device__ __forceinline__ void load_rows4_async(FA3_LDS char* rows, const Fused
 
 // Direct-to-LDS copy of the row statistics of 64 query rows starting at row0;
 // every wave issues exactly one load (one dword per active lane).
-//   kRows 0: lse2 -> rows[0..64), -delta -> rows[64..128); wave w, lanes 0..15.
+//   kRows 0: -lse2 -> rows[0..64), -delta -> rows[64..128); wave w, lanes 0..15.
 //   kRows 1: packed[3 row0 .. 3 row0 + 192) -> rows[0..192) ([row][3]);
 //            wave w, lanes 0..23 move dwords 24 w .. 24 w + 23.
 //   kRows 2: max -> rows[0..64), sum -> rows[64..128), delta -> rows[128..192);
@@ -266,7 +274,7 @@ template <int kRows>
 __device__ __forceinline__ void load_rows_async(FA3_LDS char* rows, const FusedArgs& a,
                                                 size_t row0, int w, int lane) {
     if constexpr (kRows == 0) {
-        const float* src = (w < 4 ? a.lse2 : a.ndelta) + row0 + 16 * (w & 3) + lane;
+        const float* src = (w < 4 ? a.nlse2 : a.ndelta) + row0 + 16 * (w & 3) + lane;
         FA3_LDS char* dst = rows + 256 * (w >> 2) + 64 * (w & 3);
         if (lane < 16)
             __builtin_amdgcn_global_load_lds((const void*)src, (FA3_LDS void*)dst, 4, 0, 0);
@@ -286,6 +294,31 @@ __device__ __forceinline__ void load_rows_async(FA3_LDS char* rows, const FusedA
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// the 16-bit operand type (f16 bits) -> fp32
+template <bool kBf16>
+__device__ __forceinline__ float from16(_Float16 x) {
+    if constexpr (kBf16) return (float)__builtin_bit_cast(__bf16, x);
+    else return (float)x;
+}
+
+// Multiplies by c (fp32 product, one rounding to the tile's type) the chunks
+// of a tile that loader ld's load_tile_async copied into LDS: each lane reads
+// back exactly the 16 bytes its own direct-to-LDS load wrote, so this wave's
+// vmcnt wait for those loads orders it and no barrier is needed.  The
+// caller's lgkmcnt wait and barrier publish the result.
+template <bool kBf16, int N>
+__device__ __forceinline__ void scale_own_chunks(FA3_LDS char* tile, int ld, int lane, float c) {
+    f16x8 v[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = lds_read_b128(tile, (ld * N + j) * 1024 + lane * 16);
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[j][e] = to16<kBf16>(from16<kBf16>(v[j][e]) * c);
+        lds_write_b128(tile, (ld * N + j) * 1024 + lane * 16, v[j]);
+    }
+}
 
 // Wave issue priority, pinned in program order.  A score wave runs its LDS
 // reads and S / dP MFMAs at raised priority: its MFMAs then win the SIMD's
@@ -653,10 +686,11 @@ __device__ __forceinline__ bool split_end(const A& a, int job, FA3_LDS int* flag
 // Streams query tiles [qa, qb) of every query head of the group.  slot < 0:
 // the job is whole and writes dK / dV; otherwise the unit is piece slot & 1
 // of split job slot >> 1 and the pieces' partial sums meet in split_end.
-template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false>
+template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false,
+          bool kScaled = true>
 __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, int slot,
                          FA3_LDS char* smem) {
-    static_assert(kRows == 0 || kRows == 1, "dKV rows come as lse2/-delta or packed");
+    static_assert(kRows == 0 || kRows == 1, "dKV rows come as -lse2/-delta or packed");
     using C = Cfg<D>;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -730,20 +764,27 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
     FA3_LDS int* flag = (FA3_LDS int*)(smem + C::kFlagOff);
     FA3_LDS char* pds1 = pds0 + 2 * C::kPdsBytes;
     auto prologue_loads = [&]() {
-        // this key tile's K and V are staged in the P / dS area
+        // this key tile's K (times c when kScaled) and V are staged in the
+        // P / dS area
         const size_t k0 = kv_elem<D>(a, b, hkv, kbase);
         load_tile_async(pds0, a.k + k0, kv_off, w);
         load_tile_async(pds0 + C::kTileBytes, a.v + k0, kv_off, w);
-        // wait for K and V only: the score waves copy them into registers
-        // while the first streamed tile lands (the prologues wait for it)
         if (loads) {
             issue(st_ld);
             issue(st_1);
             issue(st_2);
-            wait_vm_lgkm0<3 * C::kDmaKv>();
-        } else {
-            wait_vm_lgkm0<0>();
         }
+        if constexpr (kScaled) {
+            // this wave's K loads have landed once only the later ones (V,
+            // the three stages) may be in flight
+            if (loads) wait_vm_lgkm0<C::kLoadsPerTile + 3 * C::kDmaKv>();
+            else wait_vm_lgkm0<C::kLoadsPerTile>();
+            scale_own_chunks<kBf16, C::kLoadsPerTile>(pds0, w, lane, a.scale_log2);
+        }
+        // wait for K and V only: the score waves copy them into registers
+        // while the first streamed tile lands (the prologues wait for it)
+        if (loads) wait_vm_lgkm0<3 * C::kDmaKv>();
+        else wait_vm_lgkm0<0>();
         barrier();
     };
 
@@ -772,13 +813,13 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                 aq[s] = lds_read_b128(st, off);
                 ad[s] = lds_read_b128(st + C::kTileBytes, off);
             }
-            f32x4 l2, ndl;  // lse2 and -delta of rows 16 t + 4 g4 + i
+            f32x4 nl2, ndl;  // -lse2 and -delta of rows 16 t + 4 g4 + i
             if constexpr (kRows == 0) {
-                // lse2 / -delta of rows 16 t .. in the layout of the loaders
+                // -lse2 / -delta of rows 16 t .. in the layout of the loaders
                 const FA3_LDS char* r =
                     st + 2 * C::kTileBytes +
                     (C::kGradLoads ? 128 * t + 16 * g4 : (16 * t + 4 * g4) * 4);
-                l2 = *(const FA3_LDS f32x4*)r;
+                nl2 = *(const FA3_LDS f32x4*)r;
                 ndl = *(const FA3_LDS f32x4*)(r + (C::kGradLoads ? 64 : 256));
             } else {
                 // [row][max_log2, inv_sum, delta]: exp2(x - m) * inv = exp2(x - (m - log2 inv))
@@ -789,7 +830,7 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
                                      r1[2], r1[3], r2[0], r2[1], r2[2], r2[3]};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    l2[i] = f[3 * i] - __log2f(f[3 * i + 1]);
+                    nl2[i] = __log2f(f[3 * i + 1]) - f[3 * i];
                     ndl[i] = -f[3 * i + 2];
                 }
             }
@@ -806,16 +847,18 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
             for (int s = 0; s < C::kKs; ++s) {
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb) {
-                    sacc[kb] = mfma_16x16x32<kBf16>(aq[s], kf[kb][s], s == 0 ? f32x4{} : sacc[kb]);
+                    sacc[kb] = mfma_16x16x32<kBf16>(aq[s], kf[kb][s],
+                                                    s != 0 ? sacc[kb] : kScaled ? nl2 : f32x4{});
                     pacc[kb] = mfma_16x16x32<kBf16>(ad[s], vf[kb][s], s == 0 ? ndl : pacc[kb]);
                 }
             }
             set_prio<0>();
+            // sacc = S c - lse2 (kScaled: K c, -lse2 seed), else S
             float p[16], ds[16];
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int kb = e >> 2, i = e & 3;
-                p[e] = fast_exp2(sacc[kb][i] * a.scale_log2 - l2[i]);
+                p[e] = fast_exp2(kScaled ? sacc[kb][i] : sacc[kb][i] * a.scale_log2 + nl2[i]);
                 ds[e] = p[e] * pacc[kb][i];
             }
             if (masked) {  // causal diagonal tile: keys after the row see nothing
@@ -994,10 +1037,11 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
 // ----------------------------------------------------------------------------
 // Streams key tiles [ka, kb) (the causal diagonal, key tile qt, is masked).
 // slot: as for dkv_role.
-template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false>
+template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false,
+          bool kScaled = true>
 __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int slot,
                         FA3_LDS char* smem) {
-    static_assert(kRows == 0 || kRows == 2, "dQ rows come as lse2/-delta or max/sum/delta");
+    static_assert(kRows == 0 || kRows == 2, "dQ rows come as -lse2/-delta or max/sum/delta");
     using C = Cfg<D>;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1052,8 +1096,9 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
     FA3_LDS int* flag = (FA3_LDS int*)(smem + C::kFlagOff);
     FA3_LDS char* ds1 = ds0 + 2 * C::kPdsBytes;
     auto prologue_loads = [&]() {
-        // this query tile's Q and dO are staged in the dS area, its lse2 and
-        // -delta in the (otherwise unused) rows slot of stage 0
+        // this query tile's Q (times c when kScaled) and dO are staged in
+        // the dS area, its -lse2 and -delta in the (otherwise unused) rows
+        // slot of stage 0
         load_tile_async(ds0, a.q + q0, q_off, w);
         load_tile_async(ds0 + C::kTileBytes, a.dout + q0, q_off, w);
         load_rows_async<kRows>(st_ld + 2 * C::kTileBytes, a, row0, w, lane);
@@ -1061,10 +1106,16 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
             issue(st_ld);
             issue(st_1);
             issue(st_2);
-            wait_vm_lgkm0<3 * C::kDmaQ>();
-        } else {
-            wait_vm_lgkm0<0>();
         }
+        if constexpr (kScaled) {
+            // this wave's Q loads have landed once only the later ones (dO,
+            // the rows' one load, the three stages) may be in flight
+            if (loads) wait_vm_lgkm0<C::kLoadsPerTile + 1 + 3 * C::kDmaQ>();
+            else wait_vm_lgkm0<C::kLoadsPerTile + 1>();
+            scale_own_chunks<kBf16, C::kLoadsPerTile>(ds0, w, lane, a.scale_log2);
+        }
+        if (loads) wait_vm_lgkm0<3 * C::kDmaQ>();
+        else wait_vm_lgkm0<0>();
         barrier();
     };
 
@@ -1074,7 +1125,7 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         // perm_row); dS goes to LDS.
         // B operands: LDS row 16 rb + l16 (query row rb + 4 l16), D chunk p1_chunk(s, g4)
         f16x8 qf[4][C::kKs], df[4][C::kKs];
-        float l2[4];
+        f32x4 nl2[4];            // -lse2 of row rb + 4 l16, the S^T accumulators' start
         f32x4 ndl[4];            // -delta of row rb + 4 l16, the dP^T accumulators' start
         f32x4 sacc[4], pacc[4];  // keys 16 t + 4 g4 + i, rows rb + 4 l16
         auto score = [&](bool masked, const FA3_LDS char* st, FA3_LDS char* ds,
@@ -1094,16 +1145,19 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
             for (int s = 0; s < C::kKs; ++s) {
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb) {
-                    sacc[rb] = mfma_16x16x32<kBf16>(ak[s], qf[rb][s], s == 0 ? f32x4{} : sacc[rb]);
+                    sacc[rb] = mfma_16x16x32<kBf16>(ak[s], qf[rb][s],
+                                                    s != 0 ? sacc[rb] : kScaled ? nl2[rb] : f32x4{});
                     pacc[rb] = mfma_16x16x32<kBf16>(av[s], df[rb][s], s == 0 ? ndl[rb] : pacc[rb]);
                 }
             }
             set_prio<0>();
+            // sacc = S^T c - lse2 (kScaled: Q c, -lse2 seed), else S^T
             float p[16];
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int rb = e >> 2, i = e & 3;
-                p[e] = fast_exp2(sacc[rb][i] * a.scale_log2 - l2[rb]) * pacc[rb][i];
+                const float x = kScaled ? sacc[rb][i] : sacc[rb][i] * a.scale_log2 + nl2[rb][0];
+                p[e] = fast_exp2(x) * pacc[rb][i];
             }
             if (masked) {  // causal diagonal tile
                 __asm__ volatile("" ::: "memory");  // keep this a branch
@@ -1130,14 +1184,15 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
                     qf[rb][s] = lds_read_b128(pa, off);
                     df[rb][s] = lds_read_b128(pa + C::kTileBytes, off);
                 }
-                float n;
+                float nl, n;
                 if constexpr (kRows == 0) {
-                    l2[rb] = rows[r];
+                    nl = rows[r];
                     n = rows[64 + r];
                 } else {  // exp2((x - max) c) / sum = exp2(x c - (max c + log2 sum))
-                    l2[rb] = rows[r] * a.scale_log2 + __log2f(rows[64 + r]);
+                    nl = -(rows[r] * a.scale_log2 + __log2f(rows[64 + r]));
                     n = -rows[128 + r];
                 }
+                nl2[rb] = f32x4{nl, nl, nl, nl};
                 ndl[rb] = f32x4{n, n, n, n};
             }
             if constexpr (C::kGradLoads) wait_vm_lgkm0<0>();  // Q / dO reads done before dS overwrites them
@@ -1299,9 +1354,14 @@ __device__ __forceinline__ void job_of(const FusedArgs& a, int& g, int& pos) {
 //
 // kSplit selects the split plan (a separate instantiation: its units issue
 // their loads at a different point of the step, see dkv_role's score).
-template <int D, bool kCausal, bool kBf16, bool kSplit>
+// kScaled: the score waves' resident operands are multiplied by scale_log2
+// (default plan, launches with scale_log2 <= 1).  The split plan keeps them
+// unscaled: its units are short (8 to 32 steps), and the scaling in each
+// unit's prologue cost about what its steps save (P3 +0.5 %).
+template <int D, bool kCausal, bool kBf16, bool kSplit, bool kScaled>
 __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     static_assert(kCausal || !kSplit, "the split plan is causal");
+    static_assert(!(kScaled && kSplit), "the split plan runs unscaled");
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
     int g, pos;
@@ -1315,42 +1375,46 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
         if (pos < M) {
             // dKV key tile M + x whole, then the remainder of dQ query tile M + x
             const int x = pos, nq = M + x + 1, lq = a.head_q[x];
-            dkv_role<D, kCausal, kBf16, 0, true>(a, g, M + x, M + x, QT, -1, smem);
+            dkv_role<D, kCausal, kBf16, 0, true, false>(a, g, M + x, M + x, QT, -1, smem);
             if (lq < nq) {
                 wait_vm_lgkm0<0>();
                 barrier();
-                dq_role<D, kCausal, kBf16, 0, true>(a, g, M + x, lq, nq, 2 * (job0 + x) + 1, smem);
+                dq_role<D, kCausal, kBf16, 0, true, false>(a, g, M + x, lq, nq, 2 * (job0 + x) + 1,
+                                                        smem);
             }
         } else if (pos < 2 * M) {
             // dQ query tile x whole, then the remainder of dKV key tile x
             const int x = pos - M, nkv = QT - x, lkv = a.head_kv[x];
-            dq_role<D, kCausal, kBf16, 0, true>(a, g, x, 0, x + 1, -1, smem);
+            dq_role<D, kCausal, kBf16, 0, true, false>(a, g, x, 0, x + 1, -1, smem);
             if (lkv < nkv) {
                 wait_vm_lgkm0<0>();
                 barrier();
-                dkv_role<D, kCausal, kBf16, 0, true>(a, g, x, x + lkv, QT, 2 * (job0 + x) + 1, smem);
+                dkv_role<D, kCausal, kBf16, 0, true, false>(a, g, x, x + lkv, QT, 2 * (job0 + x) + 1,
+                                                         smem);
             }
         } else if (pos < 3 * M) {
             // head piece (or all) of dKV key tile x
             const int x = pos - 2 * M, nkv = QT - x, lkv = a.head_kv[x];
-            dkv_role<D, kCausal, kBf16, 0, true>(a, g, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1,
-                                 smem);
+            dkv_role<D, kCausal, kBf16, 0, true, false>(a, g, x, x, x + min(lkv, nkv),
+                                                     lkv < nkv ? 2 * (job0 + x) : -1, smem);
         } else {
             // head piece (or all) of dQ query tile M + x
             const int x = pos - 3 * M, nq = M + x + 1, lq = a.head_q[x];
-            dq_role<D, kCausal, kBf16, 0, true>(a, g, M + x, 0, min(lq, nq), lq < nq ? 2 * (job0 + x) : -1, smem);
+            dq_role<D, kCausal, kBf16, 0, true, false>(a, g, M + x, 0, min(lq, nq),
+                                                    lq < nq ? 2 * (job0 + x) : -1, smem);
         }
         return;
     }
     const int level = pos / (group + 1);
     const int slot = pos % (group + 1);
     if (slot == 0) {
-        dkv_role<D, kCausal, kBf16>(a, g, level, kCausal ? level : 0, QT, -1, smem);
+        dkv_role<D, kCausal, kBf16, 0, false, kScaled>(a, g, level, kCausal ? level : 0, QT, -1,
+                                                       smem);
     } else {
         const int b = g / a.heads_kv, hkv = g % a.heads_kv;
         const int qt = QT - 1 - level;
-        dq_role<D, kCausal, kBf16>(a, b * a.heads_q + hkv * group + slot - 1, qt, 0, kCausal ? qt + 1 : QT,
-                            -1, smem);
+        dq_role<D, kCausal, kBf16, 0, false, kScaled>(a, b * a.heads_q + hkv * group + slot - 1, qt,
+                                                      0, kCausal ? qt + 1 : QT, -1, smem);
     }
 }
 
@@ -1358,6 +1422,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
 // per KV head, fp32 outputs): one job per key tile (kRole 1, row statistics
 // from the packed sidecar) or per query tile (kRole 2, from max / sum /
 // delta), longest first.  No workspace: the statistics are folded in LDS.
+// The operands stay unscaled (any softmax scale; these entries are not the
+// fast path).
 template <int D, int kRole>
 __global__ __launch_bounds__(kThreads, 1) void bwd_component_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
@@ -1366,10 +1432,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_component_kernel(FusedArgs a)
     job_of(a, g, pos);
     const int QT = a.seqlen / 64;
     if constexpr (kRole == 1) {
-        dkv_role<D, true, false, 1>(a, g, pos, pos, QT, -1, smem);
+        dkv_role<D, true, false, 1, false, false>(a, g, pos, pos, QT, -1, smem);
     } else {
         const int qt = QT - 1 - pos;
-        dq_role<D, true, false, 2>(a, g, qt, 0, qt + 1, -1, smem);
+        dq_role<D, true, false, 2, false, false>(a, g, qt, 0, qt + 1, -1, smem);
     }
 }
 
@@ -1378,14 +1444,21 @@ void launch_d(const FusedArgs& a, bool causal, bool bf16, hipStream_t stream) {
     const dim3 grid(a.n_groups * a.jobs_per_group);
     const dim3 block(kThreads);
     const bool split = a.bal_m > 0;  // causal only (plan_workspace)
+    // K c / Q c cannot overflow fp16 when c <= 1
+    const bool scaled = a.scale_log2 <= 1.f;
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream, a); };
     if (bf16) {
-        if (split) hipLaunchKernelGGL((bwd_main_kernel<D, true, true, true>), grid, block, 0, stream, a);
-        else if (causal) hipLaunchKernelGGL((bwd_main_kernel<D, true, true, false>), grid, block, 0, stream, a);
-        else hipLaunchKernelGGL((bwd_main_kernel<D, false, true, false>), grid, block, 0, stream, a);
+        if (split) go(bwd_main_kernel<D, true, true, true, false>);
+        else if (causal) go(scaled ? bwd_main_kernel<D, true, true, false, true>
+                                   : bwd_main_kernel<D, true, true, false, false>);
+        else go(scaled ? bwd_main_kernel<D, false, true, false, true>
+                       : bwd_main_kernel<D, false, true, false, false>);
     } else {
-        if (split) hipLaunchKernelGGL((bwd_main_kernel<D, true, false, true>), grid, block, 0, stream, a);
-        else if (causal) hipLaunchKernelGGL((bwd_main_kernel<D, true, false, false>), grid, block, 0, stream, a);
-        else hipLaunchKernelGGL((bwd_main_kernel<D, false, false, false>), grid, block, 0, stream, a);
+        if (split) go(bwd_main_kernel<D, true, false, true, false>);
+        else if (causal) go(scaled ? bwd_main_kernel<D, true, false, false, true>
+                                   : bwd_main_kernel<D, true, false, false, false>);
+        else go(scaled ? bwd_main_kernel<D, false, false, false, true>
+                       : bwd_main_kernel<D, false, false, false, false>);
     }
 }
 
@@ -1560,7 +1633,7 @@ WorkspacePlan plan_workspace(const BwdProblem& p) {
     const Checked rows = Checked{(size_t)p.batch}.mul((size_t)p.heads_q).mul((size_t)p.seqlen);
     Checked at{256};  // the error word's region
     w.err_off = 0;
-    w.lse2_off = at.v;
+    w.nlse2_off = at.v;
     at = at.add(rows.mul(sizeof(float)).v).align();
     w.ndelta_off = at.v;
     at = at.add(rows.mul(sizeof(float)).v).align();
@@ -1614,18 +1687,18 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     if (!plan.ok) return hipErrorInvalidValue;
     char* ws = static_cast<char*>(workspace);
     FusedArgs a = base_args(p, t);
-    float* lse2 = reinterpret_cast<float*>(ws + plan.lse2_off);
+    float* nlse2 = reinterpret_cast<float*>(ws + plan.nlse2_off);
     float* ndelta = reinterpret_cast<float*>(ws + plan.ndelta_off);
     auto mark = [&](int i) {
         return t.events[i] != nullptr ? hipEventRecord(t.events[i], t.stream) : hipSuccess;
     };
     hipError_t err = mark(0);
     if (err != hipSuccess) return err;
-    err = t.packed_in != nullptr ? launch_rowstats(p, t, lse2, ndelta)
-                                 : launch_preprocess(p, t, lse2, ndelta);
+    err = t.packed_in != nullptr ? launch_rowstats(p, t, nlse2, ndelta)
+                                 : launch_preprocess(p, t, nlse2, ndelta);
     if (err == hipSuccess) err = mark(1);
     if (err != hipSuccess) return err;
-    a.lse2 = lse2;
+    a.nlse2 = nlse2;
     a.ndelta = ndelta;
     const int group = p.heads_q / p.heads_kv;
     a.jobs_per_group = (p.seqlen / kTileN) * (1 + group);

@@ -5,9 +5,10 @@
 //   delta[r] = sum_d fp32(dO[r, d]) * fp32(O[r, d])          (fp32)
 //   lse2[r]  = LSE[r] * log2(e)                                 (LSE input)
 //            = max[r] * scale * log2(e) + log2(sum[r])          (SMAX_SSUM)
-// so the main kernel forms P = exp2(s * scale * log2(e) - lse2[r]); it also
-// takes -delta[r] (ndelta), which seeds its dP accumulators so that they end
-// at dP - delta.  Each output is optional (null pointer: not written).
+// so that P = exp2(s * scale * log2(e) - lse2[r]).  The main kernel takes
+// -lse2[r] (nlse2) and -delta[r] (ndelta), which seed its S and dP
+// accumulators so that they end at S c - lse2 and dP - delta.  Each output
+// is optional (null pointer: not written).
 // Optionally also writes the reference's packed sidecar
 // [row_max_log2, row_inv_sum, delta] (reference src/dot_do_o_kernel.cpp:49-61).
 //
@@ -26,7 +27,7 @@ template <int D, bool kLse, bool kBf16>
 __global__ __launch_bounds__(256) void preprocess_kernel(
     const _Float16* __restrict__ dout, const _Float16* __restrict__ out,
     const float* __restrict__ aux0, const float* __restrict__ aux1,
-    float* __restrict__ delta, float* __restrict__ lse2, float* __restrict__ ndelta,
+    float* __restrict__ delta, float* __restrict__ nlse2, float* __restrict__ ndelta,
     float* __restrict__ packed, int rows,
     float scale_log2, int heads_q, int seqlen, int q_rs, int q_hs) {
     constexpr int kLanesPerRow = D / 8;
@@ -53,7 +54,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
             l2 = max_log2 + log2f(s);
         }
         if (delta != nullptr) delta[row] = acc;
-        if (lse2 != nullptr) lse2[row] = l2;
+        if (nlse2 != nullptr) nlse2[row] = -l2;
         if (ndelta != nullptr) ndelta[row] = -acc;
         if (packed != nullptr) {
             packed[(size_t)row * 3 + 0] = max_log2;
@@ -64,7 +65,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
 }
 
 template <int D>
-hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta) {
+hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* nlse2, float* ndelta) {
     constexpr int kRowsPerBlock = 256 / (D / 8);
     const int rows = p.batch * p.heads_q * p.seqlen;
     const int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
@@ -73,7 +74,7 @@ hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, f
     const int q_hs = p.bshd ? D : p.seqlen * D;
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), 0, t.stream, (const _Float16*)t.dout,
-                           (const _Float16*)t.out, t.aux0, t.aux1, t.delta, lse2, ndelta,
+                           (const _Float16*)t.out, t.aux0, t.aux1, t.delta, nlse2, ndelta,
                            t.packed, rows, scale_log2, p.heads_q, p.seqlen,
                            q_rs, q_hs);
     };
@@ -89,30 +90,30 @@ hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* lse2, f
 
 // Row statistics from the packed sidecar [max_log2, inv_sum, delta]
 // (reference src/dot_do_o_kernel.cpp:49-61) for the fused5 entry:
-// lse2 = max_log2 - log2(inv_sum), since exp2(x - m) * inv = exp2(x - (m -
+// -lse2 = log2(inv_sum) - max_log2, since exp2(x - m) * inv = exp2(x - (m -
 // log2 inv)), and -delta.
 __global__ __launch_bounds__(256) void rowstats_kernel(const float* __restrict__ packed,
-                                                       float* __restrict__ lse2,
+                                                       float* __restrict__ nlse2,
                                                        float* __restrict__ ndelta, int rows) {
     const int r = blockIdx.x * 256 + threadIdx.x;
     if (r >= rows) return;
-    lse2[r] = packed[(size_t)r * 3] - log2f(packed[(size_t)r * 3 + 1]);
+    nlse2[r] = log2f(packed[(size_t)r * 3 + 1]) - packed[(size_t)r * 3];
     ndelta[r] = -packed[(size_t)r * 3 + 2];
 }
 
 }  // namespace
 
-hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* lse2, float* ndelta) {
+hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* nlse2, float* ndelta) {
     const int rows = p.batch * p.heads_q * p.seqlen;
     hipLaunchKernelGGL(rowstats_kernel, dim3((rows + 255) / 256), dim3(256), 0, t.stream,
-                       t.packed_in, lse2, ndelta, rows);
+                       t.packed_in, nlse2, ndelta, rows);
     return hipGetLastError();
 }
 
-hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* lse2,
+hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* nlse2,
                              float* ndelta) {
-    if (p.head_dim == 128) return launch_pre_d<128>(p, t, lse2, ndelta);
-    if (p.head_dim == 64) return launch_pre_d<64>(p, t, lse2, ndelta);
+    if (p.head_dim == 128) return launch_pre_d<128>(p, t, nlse2, ndelta);
+    if (p.head_dim == 64) return launch_pre_d<64>(p, t, nlse2, ndelta);
     return hipErrorInvalidValue;
 }
 

@@ -58,6 +58,27 @@ def test_v2_matches_oracle(B, Hq, Hkv, S, D, causal):
     log({k: (round(v["max_rel"], 6), round(v["max_abs"], 6)) for k, v in rep.items()})
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,causal,scale", [
+    (1, 2, 1, 256, 64, False, 0.75),   # c = scale log2 e > 1: unscaled instantiation
+    (1, 4, 2, 384, 128, True, 1.0),    # c > 1, causal, D = 128
+    (1, 4, 2, 384, 128, True, 0.69),   # just below ln 2: operands scaled by c = 0.995
+    (2, 4, 2, 256, 64, False, 0.02),   # small c, scaled
+    (1, 1, 1, 256, 128, True, 1.0),    # split plan (unscaled at every scale)
+])
+def test_v2_softmax_scales(B, Hq, Hkv, S, D, causal, scale):
+    """The default plan's score waves multiply their resident operand (K, or
+    Q in the dQ role) by c = scale log2 e only when c <= 1, where the product
+    cannot overflow fp16; larger scales run the unscaled instantiations,
+    which apply c in the loop.  Both sides of that threshold match the
+    oracle."""
+    log(f"[case] v2 scale={scale} B={B} Hq={Hq} Hkv={Hkv} S={S} D={D} causal={causal}")
+    g = O.golden(B, Hq, Hkv, S, D, causal, scale=scale)
+    res = run_v2(g, torch)
+    assert res["status"] == F.SUCCESS, F.status_name(res["status"])
+    rep = check(res, g)
+    log({k: (round(v["max_rel"], 6), round(v["max_abs"], 6)) for k, v in rep.items()})
+
+
 @pytest.mark.parametrize("S,causal", [(128, True), (1024, True), (256, False)])
 def test_v2_reference_pattern_inputs(S, causal):
     """The reference's own deterministic inputs (generate_full_bwd_golden.py:
