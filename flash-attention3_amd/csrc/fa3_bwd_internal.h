@@ -15,6 +15,35 @@ namespace fa3 {
 constexpr int kTileN = 64;
 constexpr int kTileM = 64;
 
+// Division by a launch-invariant divisor d (1 <= d < 2^31) of 0 <= n < 2^31
+// as a multiply-high, an add and a shift (Granlund-Montgomery round-up
+// method): with s = ceil(log2 d) and mul = floor(2^32 (2^s - d) / d) + 1,
+// n / d = (mulhi(n, mul) + n) >> s.  The host computes mul and s once per
+// launch; in the kernels the operands are wave-uniform, so a quotient costs
+// three scalar instructions instead of a ~30-instruction division sequence
+// that all 8 waves of a workgroup would run on the CU's one scalar unit.
+struct FastDiv {
+    uint32_t mul = 1;
+    uint32_t shr = 0;
+    int d = 1;
+};
+
+inline FastDiv make_fastdiv(int d) {
+    FastDiv f;
+    if (d < 1) d = 1;  // unused divisor slot
+    f.d = d;
+    uint32_t s = 0;
+    while (s < 31 && (1u << s) < (uint32_t)d) ++s;
+    f.shr = s;
+    f.mul = (uint32_t)(((uint64_t)1 << 32) * (((uint64_t)1 << s) - (uint64_t)d) / (uint64_t)d + 1);
+    return f;
+}
+
+__host__ __device__ inline int fdiv(const FastDiv& f, int n) {
+    const uint32_t hi = (uint32_t)(((uint64_t)(uint32_t)n * f.mul) >> 32);
+    return (int)((hi + (uint32_t)n) >> f.shr);
+}
+
 // Everything a backward launch needs, already validated and resolved
 // (default scale applied, aux mode folded into the lse2 preprocessing).
 struct BwdProblem {

@@ -93,6 +93,10 @@ struct FusedArgs {
     int seqlen;
     int heads_q;
     int heads_kv;
+    int group;  // heads_q / heads_kv
+    // divisors of the kernels' index arithmetic (FastDiv: magic multipliers
+    // computed once on the host)
+    FastDiv div_hq, div_hkv, div_group, div_g1;  // heads_q, heads_kv, group, group + 1
     // job map: n_groups (batch, kv head) groups of jobs_per_group jobs; with
     // xcd_parts > 0 each group is split into xcd_parts interleaved parts of
     // part_len jobs and whole parts are pinned to one XCD.
@@ -100,6 +104,7 @@ struct FusedArgs {
     int jobs_per_group;
     int xcd_parts;
     int part_len;
+    FastDiv div_parts, div_part_len, div_jpg;  // xcd_parts, part_len, jobs_per_group
     float scale_log2;
     float scale;
     // split plan (bal_m > 0, causal and one query head per KV head): see
@@ -454,7 +459,7 @@ __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase
                                           const f32x16 (&acc)[D / 64][2], FA3_LDS char* stage) {
     constexpr int kPpw = D / 64;
     const int l32 = lane & 31, h = lane >> 5;
-    const int b = bkv / a.heads_kv;
+    const int b = fdiv(a.div_hkv, bkv);
     const size_t base = kv_elem<D>(a, b, bkv - b * a.heads_kv, kbase);
     if (!a.out_f32) {
         const float mul = (t >> 1) == 0 ? 1.f : a.scale;
@@ -700,9 +705,9 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
 
     const int S = a.seqlen;
     const int QT = S / 64;
-    const int group = a.heads_q / a.heads_kv;
-    const int b = bkv / a.heads_kv;
-    const int hkv = bkv % a.heads_kv;
+    const int group = a.group;
+    const int b = fdiv(a.div_hkv, bkv);
+    const int hkv = bkv - b * a.heads_kv;
     const int kbase = kt * 64;
     const int n_it = group * (qb - qa);
 
@@ -1051,10 +1056,10 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
 
     const int S = a.seqlen;
     const int QT = S / 64;
-    const int group = a.heads_q / a.heads_kv;
-    const int b = bhq / a.heads_q;
+    const int group = a.group;
+    const int b = fdiv(a.div_hq, bhq);
     const int hq = bhq - b * a.heads_q;
-    const int hkv = hq / group;
+    const int hkv = fdiv(a.div_group, hq);
     const size_t row0 = (size_t)bhq * S + qt * 64;  // statistics row
     const size_t q0 = q_elem<D>(a, b, hq, qt * 64);  // this tile's Q / dO / dQ elements
     const int n_kt = kb - ka;
@@ -1316,12 +1321,13 @@ __device__ __forceinline__ void job_of(const FusedArgs& a, int& g, int& pos) {
     if (a.xcd_parts > 0) {
         const int xcd = id & 7;
         const int n = id >> 3;
-        const int v = xcd + 8 * (n / a.part_len);  // virtual group = (group, part)
-        g = v / a.xcd_parts;
-        pos = v % a.xcd_parts + a.xcd_parts * (n % a.part_len);
+        const int nq = fdiv(a.div_part_len, n);
+        const int v = xcd + 8 * nq;  // virtual group = (group, part)
+        g = fdiv(a.div_parts, v);
+        pos = v - g * a.xcd_parts + a.xcd_parts * (n - nq * a.part_len);
     } else {
-        g = id / a.jobs_per_group;
-        pos = id % a.jobs_per_group;
+        g = fdiv(a.div_jpg, id);
+        pos = id - g * a.jobs_per_group;
     }
 }
 
@@ -1366,7 +1372,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
     int g, pos;
     job_of(a, g, pos);
-    const int group = a.heads_q / a.heads_kv;
+    const int group = a.group;
     const int QT = a.seqlen / 64;
     if constexpr (kSplit) {
         // G = 1: group g is query head g (and KV head g)
@@ -1405,13 +1411,13 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
         }
         return;
     }
-    const int level = pos / (group + 1);
-    const int slot = pos % (group + 1);
+    const int level = fdiv(a.div_g1, pos);
+    const int slot = pos - level * (group + 1);
     if (slot == 0) {
         dkv_role<D, kCausal, kBf16, 0, false, kScaled>(a, g, level, kCausal ? level : 0, QT, -1,
                                                        smem);
     } else {
-        const int b = g / a.heads_kv, hkv = g % a.heads_kv;
+        const int b = fdiv(a.div_hkv, g), hkv = g - b * a.heads_kv;
         const int qt = QT - 1 - level;
         dq_role<D, kCausal, kBf16, 0, false, kScaled>(a, b * a.heads_q + hkv * group + slot - 1, qt,
                                                       0, kCausal ? qt + 1 : QT, -1, smem);
@@ -1470,6 +1476,9 @@ void set_job_map(FusedArgs& a) {
     const bool fits = a.jobs_per_group % parts == 0;
     a.xcd_parts = fits ? parts : 0;
     a.part_len = fits ? a.jobs_per_group / parts : 0;
+    a.div_parts = make_fastdiv(a.xcd_parts);
+    a.div_part_len = make_fastdiv(a.part_len);
+    a.div_jpg = make_fastdiv(a.jobs_per_group);
 }
 
 // Head-piece lengths of the split plan.  Workgroup times in units of one dKV
@@ -1544,6 +1553,11 @@ FusedArgs base_args(const BwdProblem& p, const BwdTensors& t) {
     a.seqlen = p.seqlen;
     a.heads_q = p.heads_q;
     a.heads_kv = p.heads_kv;
+    a.group = p.heads_q / p.heads_kv;
+    a.div_hq = make_fastdiv(p.heads_q);
+    a.div_hkv = make_fastdiv(p.heads_kv);
+    a.div_group = make_fastdiv(a.group);
+    a.div_g1 = make_fastdiv(a.group + 1);
     a.n_groups = p.batch * p.heads_kv;
     a.scale_log2 = p.scale * kLog2e;
     a.scale = p.scale;

@@ -2,7 +2,8 @@
 and UndefinedBehaviorSanitizer while a fuzzer drives every validation,
 workspace query and entry point with random parameter structs
 (tests/sanitize/abi_fuzz.cpp), and the CPU oracle under ASan + UBSan and
-under ThreadSanitizer (tests/sanitize/oracle_run.cpp).  Built by
+under ThreadSanitizer (tests/sanitize/oracle_run.cpp), and the kernels'
+host-computed fast division against / under UBSan (tests/sanitize/fastdiv_check.cpp).  Built by
 tests/sanitize/Makefile."""
 import os
 import shutil
@@ -27,7 +28,7 @@ def built():
 
 
 @pytest.mark.parametrize("exe,args", [("abi_asan", ["20000"]), ("oracle_asan", []),
-                                      ("oracle_tsan", [])])
+                                      ("oracle_tsan", []), ("fastdiv_ubsan", [])])
 def test_sanitized_run_is_clean(built, exe, args):
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1",
                UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1",
