@@ -15,6 +15,13 @@ namespace fa3 {
 constexpr int kTileN = 64;
 constexpr int kTileM = 64;
 
+// Job queues of the persistent main kernel: one counter per XCD (workgroup
+// id % 8), each on its own 128-byte line of the workspace, zeroed by the
+// preprocess pass that runs before the main kernel.
+constexpr int kQueues = 8;
+constexpr int kQueueStride = 32;  // 32-bit words between counters
+constexpr size_t kQueueBytes = (size_t)kQueues * kQueueStride * 4;
+
 // Division by a launch-invariant divisor d (1 <= d < 2^31) of 0 <= n < 2^31
 // as a multiply-high, an add and a shift (Granlund-Montgomery round-up
 // method): with s = ceil(log2 d) and mul = floor(2^32 (2^s - d) / d) + 1,
@@ -99,6 +106,7 @@ struct WorkspacePlan {
     size_t err_off = 0;
     size_t nlse2_off = 0;
     size_t ndelta_off = 0;
+    size_t queue_off = 0;   // kQueueBytes of job-queue counters
     int bal_m = 0;          // > 0: split plan with M = bal_m
     int n_split = 0;        // split jobs per role
     size_t sync_off = 0;
@@ -119,13 +127,14 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
 
 // Delta preprocess: delta into t.delta, -lse2 and -delta into the given rows;
 // any of the three may be null.  Alone, it is the component entry
-// shaobo_fa3_bwd_dot_do_o.
+// shaobo_fa3_bwd_dot_do_o.  queue (optional): the main kernel's job-queue
+// counters, zeroed.
 hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* nlse2,
-                             float* ndelta);
+                             float* ndelta, unsigned int* queue = nullptr);
 
-// -lse2 and -delta rows from the packed sidecar t.packed_in.
+// -lse2 and -delta rows from the packed sidecar t.packed_in; queue as above.
 hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* nlse2,
-                           float* ndelta);
+                           float* ndelta, unsigned int* queue = nullptr);
 
 // Workspace-free single-role components (causal, heads_q == heads_kv, fp32
 // outputs when p.out_f32): role 1 writes dK / dV from t.packed_in, role 2

@@ -105,6 +105,15 @@ struct FusedArgs {
     int xcd_parts;
     int part_len;
     FastDiv div_parts, div_part_len, div_jpg;  // xcd_parts, part_len, jobs_per_group
+    // Persistent default plan (persist > 0): the grid has persist workgroups
+    // (a multiple of 8, one per CU).  Job ids of the map above are dealt to
+    // queues by id % 8 (the XCD the hardware would have sent them to);
+    // workgroup w runs id w first, then pops k = 0, 1, .. from queue w % 8
+    // (a counter in the workspace, zeroed by the preprocess) and runs id
+    // w % 8 + 8 (k + persist / 8), until the id reaches n_jobs.
+    int persist;
+    int n_jobs;
+    unsigned int* queue;
     float scale_log2;
     float scale;
     // split plan (bal_m > 0, causal and one query head per KV head): see
@@ -129,6 +138,20 @@ struct FusedArgs {
     uint32_t part_kv_bytes;
     uint32_t part_q_bytes;
 };
+
+// The kernel arguments where the launch put them, in the kernel-argument
+// segment (constant address space, scalar loads).  The persistent job loop
+// reads a job's set-up values (the divisors of the job map) through this
+// pointer after an empty asm, so that the compiler re-reads them per job
+// instead of holding them in scalar registers across both roles' code.
+typedef __attribute__((address_space(4))) const FusedArgs KArgs;
+__device__ __forceinline__ KArgs& kargs() {
+    return *(KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+}
+// a divisor read from the argument segment
+__host__ __device__ __forceinline__ int fdiv(__attribute__((address_space(4))) const FastDiv& f, int n) {
+    return fdiv(FastDiv{f.mul, f.shr, f.d}, n);
+}
 
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kWave;
@@ -325,6 +348,16 @@ __device__ __forceinline__ void scale_own_chunks(FA3_LDS char* tile, int ld, int
     }
 }
 
+// threadIdx.x as a value the compiler cannot hoist out of a loop: in the
+// persistent kernel's job loop, per-lane values derived from it (load
+// offsets and the like) are then recomputed per job instead of being held in
+// registers across both roles' code.
+__device__ __forceinline__ int opaque_tid() {
+    int tid = threadIdx.x;
+    __asm__ volatile("" : "+v"(tid));
+    return tid;
+}
+
 // Wave issue priority, pinned in program order.  A score wave runs its LDS
 // reads and S / dP MFMAs at raised priority: its MFMAs then win the SIMD's
 // matrix unit over the gradient wave's, so its softmax and P / dS writes
@@ -384,11 +417,11 @@ __device__ __forceinline__ f16x8 swap_halves(f16x8 x) {
 }
 // Element offset of sequence row s of head h in batch b.
 template <int D>
-__device__ __forceinline__ size_t q_elem(const FusedArgs& a, int b, int h, int s) {
+__device__ __forceinline__ size_t q_elem(KArgs& a, int b, int h, int s) {
     return (size_t)b * a.heads_q * a.seqlen * D + (size_t)h * a.q_hs + (size_t)s * a.q_rs;
 }
 template <int D>
-__device__ __forceinline__ size_t kv_elem(const FusedArgs& a, int b, int h, int s) {
+__device__ __forceinline__ size_t kv_elem(KArgs& a, int b, int h, int s) {
     return (size_t)b * a.heads_kv * a.seqlen * D + (size_t)h * a.kv_hs + (size_t)s * a.kv_rs;
 }
 
@@ -398,7 +431,7 @@ __device__ __forceinline__ size_t kv_elem(const FusedArgs& a, int b, int h, int 
 // Four consecutive output elements (element offset `off`): the inputs'
 // 16-bit type, or fp32.
 template <bool kBf16>
-__device__ __forceinline__ void store4(const FusedArgs& a, void* base, size_t off, f32x4 v) {
+__device__ __forceinline__ void store4(KArgs& a, void* base, size_t off, f32x4 v) {
     if (a.out_f32) {
         *(f32x4*)((float*)base + off) = v;
     } else {
@@ -449,18 +482,17 @@ __device__ __forceinline__ int stage64_row(int j, int lane) {
 }
 
 // dV^T / dK^T accumulators of gradient wave t (pairs dkv_pair(t, u)) to dV /
-// dK of KV head bkv, keys kbase ..; lane: key 32 kb + l32,
+// dK of KV head hkv of batch b, keys kbase ..; lane: key 32 kb + l32,
 // d = 32 slice + 8 (i / 4) + 4 h + i % 4.  The wave's pairs share one matrix
 // and cover D columns d0 .. d0 + 32 kPpw of all 64 keys; 16-bit outputs are
 // transposed through the wave's own 8 KiB (D 64: 4 KiB) of `stage` so that
 // every global store writes whole 128-byte (D 64: 64-byte) row segments.
 template <int D, bool kBf16>
-__device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase, int t, int lane,
+__device__ __forceinline__ void store_dkv(KArgs& a, int b, int hkv, int kbase, int t, int lane,
                                           const f32x16 (&acc)[D / 64][2], FA3_LDS char* stage) {
     constexpr int kPpw = D / 64;
     const int l32 = lane & 31, h = lane >> 5;
-    const int b = fdiv(a.div_hkv, bkv);
-    const size_t base = kv_elem<D>(a, b, bkv - b * a.heads_kv, kbase);
+    const size_t base = kv_elem<D>(a, b, hkv, kbase);
     if (!a.out_f32) {
         const float mul = (t >> 1) == 0 ? 1.f : a.scale;
         _Float16* outp = (_Float16*)((t >> 1) == 0 ? a.dv : a.dk);
@@ -521,7 +553,7 @@ __device__ __forceinline__ void store_dkv(const FusedArgs& a, int bkv, int kbase
 // outputs go through the wave's 4 KiB (D 64: 2 KiB) of `stage`, so every
 // global store writes whole 64-byte row segments.
 template <int D, bool kBf16>
-__device__ __forceinline__ void store_dq(const FusedArgs& a, size_t base, int t, int lane,
+__device__ __forceinline__ void store_dq(KArgs& a, size_t base, int t, int lane,
                                          const f32x16 (&acc)[D / 64], FA3_LDS char* stage) {
     constexpr int kRb = D / 64;
     const int db = D == 128 ? t : t >> 1;
@@ -688,35 +720,44 @@ __device__ __forceinline__ bool split_end(const A& a, int job, FA3_LDS int* flag
 // ----------------------------------------------------------------------------
 // dKV role
 // ----------------------------------------------------------------------------
-// Streams query tiles [qa, qb) of every query head of the group.  slot < 0:
+// Key tile kt of KV head hkv in batch b.  Streams query tiles [qa, qb) of
+// every query head of the group.  slot < 0:
 // the job is whole and writes dK / dV; otherwise the unit is piece slot & 1
 // of split job slot >> 1 and the pieces' partial sums meet in split_end.
 template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false,
           bool kScaled = true>
-__device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, int slot,
+__device__ __forceinline__ void dkv_role(const FusedArgs& a, KArgs& d, int b, int hkv, int kt, int qa, int qb,
+                                         int slot,
                          FA3_LDS char* smem) {
     static_assert(kRows == 0 || kRows == 1, "dKV rows come as -lse2/-delta or packed");
     using C = Cfg<D>;
-    const int tid = threadIdx.x;
+    const int tid = opaque_tid();
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t = w & 3;
     const int l16 = lane & 15, g4 = lane >> 4, l32 = lane & 31, h = lane >> 5;
 
-    const int S = a.seqlen;
+    const int S = d.seqlen;
     const int QT = S / 64;
-    const int group = a.group;
-    const int b = fdiv(a.div_hkv, bkv);
-    const int hkv = bkv - b * a.heads_kv;
+    const int group = d.group;
     const int kbase = kt * 64;
     const int n_it = group * (qb - qa);
 
     // loader index of this wave when it loads (see Cfg::kGradLoads)
     const int ldr = C::kGradLoads ? t : w;
     const bool loads = !C::kGradLoads || w >= 4;
+    FA3_LDS char* pds0 = smem + C::kPdsOff;
+    // this key tile's K (times c when kScaled, below) and V are staged in the
+    // P / dS area; their loads go out before the rest of the set-up
     uint32_t ld_off[C::kNld], kv_off[C::kLoadsPerTile];
-    tile_load_offsets<D, C::kNld>(ld_off, ldr, lane, a.q_rs);
-    tile_load_offsets<D, C::kLoadsPerTile, true>(kv_off, w, lane, a.kv_rs);
+    tile_load_offsets<D, C::kLoadsPerTile, true>(kv_off, w, lane, d.kv_rs);
+    {
+        const size_t k0 = kv_elem<D>(d, b, hkv, kbase);
+        load_tile_async(pds0, d.k + k0, kv_off, w);
+        load_tile_async(pds0 + C::kTileBytes, d.v + k0, kv_off, w);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    tile_load_offsets<D, C::kNld>(ld_off, ldr, lane, d.q_rs);
 
     // Cursor of the next query tile to load; a finished stream keeps
     // re-loading its last tile (into a stage nobody reads), so every step
@@ -724,10 +765,10 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
     // statistics-row offsets, so a step's issue is a few adds.)
     int ld_qt = qa, ld_left = n_it;
     const int h0 = hkv * group;
-    size_t ld_e = q_elem<D>(a, b, h0, qa * 64);                  // Q / dO element
-    size_t ld_row = ((size_t)b * a.heads_q + h0) * S + qa * 64;  // statistics row
-    const size_t step_e = (size_t)64 * a.q_rs;
-    const size_t wrap_e = (size_t)a.q_hs - (size_t)(qb - qa - 1) * step_e;  // next head, tile qa
+    size_t ld_e = q_elem<D>(d, b, h0, qa * 64);                  // Q / dO element
+    size_t ld_row = ((size_t)b * d.heads_q + h0) * S + qa * 64;  // statistics row
+    const size_t step_e = (size_t)64 * d.q_rs;
+    const size_t wrap_e = (size_t)d.q_hs - (size_t)(qb - qa - 1) * step_e;  // next head, tile qa
     const size_t wrap_row = (size_t)S - (size_t)(qb - qa - 1) * 64;
     auto issue = [&](FA3_LDS char* st) {  // loading waves
         load_tile_async(st, a.q + ld_e, ld_off, ldr);
@@ -765,15 +806,10 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         st_1 = st_2;
         st_2 = x;
     };
-    FA3_LDS char* pds0 = smem + C::kPdsOff;
     FA3_LDS int* flag = (FA3_LDS int*)(smem + C::kFlagOff);
     FA3_LDS char* pds1 = pds0 + 2 * C::kPdsBytes;
     auto prologue_loads = [&]() {
-        // this key tile's K (times c when kScaled) and V are staged in the
-        // P / dS area
-        const size_t k0 = kv_elem<D>(a, b, hkv, kbase);
-        load_tile_async(pds0, a.k + k0, kv_off, w);
-        load_tile_async(pds0 + C::kTileBytes, a.v + k0, kv_off, w);
+        // K and V are on their way (issued at the top); the stages follow
         if (loads) {
             issue(st_ld);
             issue(st_1);
@@ -926,8 +962,8 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         if (j + 1 < n_it) step(st_ld, st_1, pds1);
         top();  // matches the gradient waves' last phase
         if (slot >= 0) {
-            split_arrive(a, slot >> 1, flag);
-            split_end(a, slot >> 1, flag, [] {});
+            split_arrive(d, slot >> 1, flag);
+            split_end(d, slot >> 1, flag, [] {});
         }
     } else {
         // ---- gradient waves: dV^T and dK^T for D slice(s); wave t owns the
@@ -1022,17 +1058,17 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
         // issue (into st_ld, or st_2 after a rotate) may still be landing, so
         // it stages the outputs
         if (slot < 0) {
-            store_dkv<D, kBf16>(a, bkv, kbase, t, lane, acc, st_1);
+            store_dkv<D, kBf16>(d, b, hkv, kbase, t, lane, acc, st_1);
             return;
         }
         // partial sums of the first piece: [job][wave][2 kPpw accumulator blocks]
         constexpr int kBlk = 2 * kPpw;
-        const __amdgpu_buffer_rsrc_t pr = partial_rsrc(a.part_kv, a.part_kv_bytes);
+        const __amdgpu_buffer_rsrc_t pr = partial_rsrc(d.part_kv, d.part_kv_bytes);
         const uint32_t part = (uint32_t)((slot >> 1) * 4 + t) * (kBlk * 4096);
         f32x16* flat = &acc[0][0];
-        if (split_end(a, slot >> 1, flag, [&] { put_partials<kBlk>(pr, part, flat, lane); })) {
+        if (split_end(d, slot >> 1, flag, [&] { put_partials<kBlk>(pr, part, flat, lane); })) {
             add_partials<kBlk>(pr, part, flat, lane);
-            store_dkv<D, kBf16>(a, bkv, kbase, t, lane, acc, st_1);
+            store_dkv<D, kBf16>(d, b, hkv, kbase, t, lane, acc, st_1);
         }
     }
 }
@@ -1040,40 +1076,47 @@ __device__ void dkv_role(const FusedArgs& a, int bkv, int kt, int qa, int qb, in
 // ----------------------------------------------------------------------------
 // dQ role
 // ----------------------------------------------------------------------------
-// Streams key tiles [ka, kb) (the causal diagonal, key tile qt, is masked).
-// slot: as for dkv_role.
+// Query tile qt of query head hq (KV head hkv) in batch b.  Streams key
+// tiles [ka, kb) (the causal diagonal, key tile qt, is masked).  slot: as
+// for dkv_role.
 template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false,
           bool kScaled = true>
-__device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int slot,
+__device__ __forceinline__ void dq_role(const FusedArgs& a, KArgs& d, int b, int hq, int hkv, int qt, int ka,
+                                        int kb, int slot,
                         FA3_LDS char* smem) {
     static_assert(kRows == 0 || kRows == 2, "dQ rows come as -lse2/-delta or max/sum/delta");
     using C = Cfg<D>;
-    const int tid = threadIdx.x;
+    const int tid = opaque_tid();
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t = w & 3;
     const int l16 = lane & 15, g4 = lane >> 4, l32 = lane & 31, h = lane >> 5;
 
-    const int S = a.seqlen;
+    const int S = d.seqlen;
     const int QT = S / 64;
-    const int group = a.group;
-    const int b = fdiv(a.div_hq, bhq);
-    const int hq = bhq - b * a.heads_q;
-    const int hkv = fdiv(a.div_group, hq);
-    const size_t row0 = (size_t)bhq * S + qt * 64;  // statistics row
-    const size_t q0 = q_elem<D>(a, b, hq, qt * 64);  // this tile's Q / dO / dQ elements
+    const int group = d.group;
+    const size_t row0 = ((size_t)b * d.heads_q + hq) * S + qt * 64;  // statistics row
+    const size_t q0 = q_elem<D>(d, b, hq, qt * 64);  // this tile's Q / dO / dQ elements
     const int n_kt = kb - ka;
 
     const int ldr = C::kGradLoads ? t : w;  // as in dkv_role
     const bool loads = !C::kGradLoads || w >= 4;
+    FA3_LDS char* ds0 = smem + C::kPdsOff;
+    // this query tile's Q (times c when kScaled, below) and dO are staged in
+    // the dS area, its -lse2 and -delta in the (otherwise unused) rows slot
+    // of stage 0; these loads go out before the rest of the set-up
     uint32_t ld_off[C::kNld], q_off[C::kLoadsPerTile];
-    tile_load_offsets<D, C::kNld>(ld_off, ldr, lane, a.kv_rs);
-    tile_load_offsets<D, C::kLoadsPerTile, true>(q_off, w, lane, a.q_rs);
-    const _Float16* kh = a.k + kv_elem<D>(a, b, hkv, 0);
-    const _Float16* vh = a.v + kv_elem<D>(a, b, hkv, 0);
+    tile_load_offsets<D, C::kLoadsPerTile, true>(q_off, w, lane, d.q_rs);
+    load_tile_async(ds0, a.q + q0, q_off, w);
+    load_tile_async(ds0 + C::kTileBytes, a.dout + q0, q_off, w);
+    load_rows_async<kRows>(smem + 2 * C::kTileBytes, a, row0, w, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    tile_load_offsets<D, C::kNld>(ld_off, ldr, lane, d.kv_rs);
+    const _Float16* kh = d.k + kv_elem<D>(d, b, hkv, 0);
+    const _Float16* vh = d.v + kv_elem<D>(d, b, hkv, 0);
     int ld_kt = ka;
-    size_t ld_e = (size_t)ka * 64 * a.kv_rs;
-    const size_t step_e = (size_t)64 * a.kv_rs;
+    size_t ld_e = (size_t)ka * 64 * d.kv_rs;
+    const size_t step_e = (size_t)64 * d.kv_rs;
     auto issue = [&](FA3_LDS char* st) {  // loading waves
         load_tile_async(st, kh + ld_e, ld_off, ldr);
         load_tile_async(st + C::kTileBytes, vh + ld_e, ld_off, ldr);
@@ -1097,16 +1140,10 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         st_1 = st_2;
         st_2 = x;
     };
-    FA3_LDS char* ds0 = smem + C::kPdsOff;
     FA3_LDS int* flag = (FA3_LDS int*)(smem + C::kFlagOff);
     FA3_LDS char* ds1 = ds0 + 2 * C::kPdsBytes;
     auto prologue_loads = [&]() {
-        // this query tile's Q (times c when kScaled) and dO are staged in
-        // the dS area, its -lse2 and -delta in the (otherwise unused) rows
-        // slot of stage 0
-        load_tile_async(ds0, a.q + q0, q_off, w);
-        load_tile_async(ds0 + C::kTileBytes, a.dout + q0, q_off, w);
-        load_rows_async<kRows>(st_ld + 2 * C::kTileBytes, a, row0, w, lane);
+        // Q, dO and the rows are on their way (issued at the top)
         if (loads) {  // as in dkv_role: Q, dO and the rows first
             issue(st_ld);
             issue(st_1);
@@ -1226,8 +1263,8 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         if (j + 1 < n_kt) step(kCausal && ka + j + 1 == qt, st_ld, st_1, ds1);
         top();  // matches the gradient waves' last phase
         if (slot >= 0) {
-            split_arrive(a, a.n_split + (slot >> 1), flag);
-            split_end(a, a.n_split + (slot >> 1), flag, [] {});
+            split_arrive(d, d.n_split + (slot >> 1), flag);
+            split_end(d, d.n_split + (slot >> 1), flag, [] {});
         }
     } else {
         // ---- gradient waves: dQ^T slice(s) over query rows; D = 128: slice
@@ -1301,23 +1338,38 @@ __device__ void dq_role(const FusedArgs& a, int bhq, int qt, int ka, int kb, int
         }
         // st_1 is free now (see dkv_role) and stages the outputs
         if (slot < 0) {
-            store_dq<D, kBf16>(a, q0, t, lane, acc, st_1);
+            store_dq<D, kBf16>(d, q0, t, lane, acc, st_1);
             return;
         }
         // partial sums of the first piece: [job][wave][kRb accumulator blocks]
-        const __amdgpu_buffer_rsrc_t pr = partial_rsrc(a.part_q, a.part_q_bytes);
+        const __amdgpu_buffer_rsrc_t pr = partial_rsrc(d.part_q, d.part_q_bytes);
         const uint32_t part = (uint32_t)((slot >> 1) * 4 + t) * (kRb * 4096);
-        if (split_end(a, a.n_split + (slot >> 1), flag,
+        if (split_end(d, d.n_split + (slot >> 1), flag,
                       [&] { put_partials<kRb>(pr, part, acc, lane); })) {
             add_partials<kRb>(pr, part, acc, lane);
-            store_dq<D, kBf16>(a, q0, t, lane, acc, st_1);
+            store_dq<D, kBf16>(d, q0, t, lane, acc, st_1);
         }
     }
 }
 
-// Block id -> (group, position in the group); see the job map below.
-__device__ __forceinline__ void job_of(const FusedArgs& a, int& g, int& pos) {
-    const int id = blockIdx.x;
+// Between two units of one workgroup (split plan, persistent default plan):
+// every wave's LDS accesses are done and every load of the first unit has
+// landed, but the gradient waves' output stores -- the last kStores
+// vector-memory operations they issued -- may still be in flight: the
+// vector-memory operations of a wave complete in issue order, so
+// vmcnt(kStores) covers every load before them.  kStores is at most the
+// number of stores the first unit's epilogue issues (store_dkv: 4 (D / 64),
+// store_dq: 2 (D / 64), more with fp32 outputs).  The score waves wait for
+// everything (their only stores are the split words and the queue pop).
+template <int kStores>
+__device__ __forceinline__ void unit_gap() {
+    if (threadIdx.x >= 4 * kWave) wait_vm_lgkm0<kStores>();
+    else wait_vm_lgkm0<0>();
+    barrier();
+}
+
+// Job id -> (group, position in the group); see the job map below.
+__device__ __forceinline__ void job_of(KArgs& a, int id, int& g, int& pos) {
     if (a.xcd_parts > 0) {
         const int xcd = id & 7;
         const int n = id >> 3;
@@ -1370,57 +1422,81 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     static_assert(!(kScaled && kSplit), "the split plan runs unscaled");
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
-    int g, pos;
-    job_of(a, g, pos);
     const int group = a.group;
     const int QT = a.seqlen / 64;
+    int g, pos;
     if constexpr (kSplit) {
-        // G = 1: group g is query head g (and KV head g)
+        job_of(kargs(), blockIdx.x, g, pos);
+        // G = 1: group g is query head g (and KV head g) of batch b
+        const int b = fdiv(kargs().div_hkv, g), h = g - b * a.heads_kv;
         const int M = a.bal_m;
         const int job0 = g * M;
         if (pos < M) {
             // dKV key tile M + x whole, then the remainder of dQ query tile M + x
             const int x = pos, nq = M + x + 1, lq = a.head_q[x];
-            dkv_role<D, kCausal, kBf16, 0, true, false>(a, g, M + x, M + x, QT, -1, smem);
+            dkv_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, M + x, M + x, QT, -1, smem);
             if (lq < nq) {
-                wait_vm_lgkm0<0>();
-                barrier();
-                dq_role<D, kCausal, kBf16, 0, true, false>(a, g, M + x, lq, nq, 2 * (job0 + x) + 1,
-                                                        smem);
+                unit_gap<4 * (D / 64)>();
+                dq_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, h, M + x, lq, nq,
+                                                        2 * (job0 + x) + 1, smem);
             }
         } else if (pos < 2 * M) {
             // dQ query tile x whole, then the remainder of dKV key tile x
             const int x = pos - M, nkv = QT - x, lkv = a.head_kv[x];
-            dq_role<D, kCausal, kBf16, 0, true, false>(a, g, x, 0, x + 1, -1, smem);
+            dq_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, h, x, 0, x + 1, -1, smem);
             if (lkv < nkv) {
-                wait_vm_lgkm0<0>();
-                barrier();
-                dkv_role<D, kCausal, kBf16, 0, true, false>(a, g, x, x + lkv, QT, 2 * (job0 + x) + 1,
-                                                         smem);
+                unit_gap<2 * (D / 64)>();
+                dkv_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, x, x + lkv, QT,
+                                                         2 * (job0 + x) + 1, smem);
             }
         } else if (pos < 3 * M) {
             // head piece (or all) of dKV key tile x
             const int x = pos - 2 * M, nkv = QT - x, lkv = a.head_kv[x];
-            dkv_role<D, kCausal, kBf16, 0, true, false>(a, g, x, x, x + min(lkv, nkv),
+            dkv_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, x, x, x + min(lkv, nkv),
                                                      lkv < nkv ? 2 * (job0 + x) : -1, smem);
         } else {
             // head piece (or all) of dQ query tile M + x
             const int x = pos - 3 * M, nq = M + x + 1, lq = a.head_q[x];
-            dq_role<D, kCausal, kBf16, 0, true, false>(a, g, M + x, 0, min(lq, nq),
+            dq_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, h, M + x, 0, min(lq, nq),
                                                     lq < nq ? 2 * (job0 + x) : -1, smem);
         }
         return;
     }
-    const int level = fdiv(a.div_g1, pos);
-    const int slot = pos - level * (group + 1);
-    if (slot == 0) {
-        dkv_role<D, kCausal, kBf16, 0, false, kScaled>(a, g, level, kCausal ? level : 0, QT, -1,
-                                                       smem);
-    } else {
-        const int b = fdiv(a.div_hkv, g), hkv = g - b * a.heads_kv;
-        const int qt = QT - 1 - level;
-        dq_role<D, kCausal, kBf16, 0, false, kScaled>(a, b * a.heads_q + hkv * group + slot - 1, qt,
-                                                      0, kCausal ? qt + 1 : QT, -1, smem);
+    // d: the argument segment, for the job's set-up (divisors); the roles
+    // read the rest from a
+    auto run = [&](KArgs& d, int id) {
+        job_of(d, id, g, pos);
+        const int level = fdiv(d.div_g1, pos);
+        const int slot = pos - level * (group + 1);
+        const int b = fdiv(d.div_hkv, g), hkv = g - b * a.heads_kv;
+        if (slot == 0) {
+            dkv_role<D, kCausal, kBf16, 0, false, kScaled>(a, d, b, hkv, level, kCausal ? level : 0,
+                                                           QT, -1, smem);
+        } else {
+            const int qt = QT - 1 - level;
+            dq_role<D, kCausal, kBf16, 0, false, kScaled>(a, d, b, hkv * group + slot - 1, hkv, qt, 0,
+                                                          kCausal ? qt + 1 : QT, -1, smem);
+        }
+    };
+    // Persistent plan: thread 0 (a score wave, done with the job before the
+    // gradient waves' last products and epilogue) pops the next id while
+    // they finish, and passes it on through LDS; the gap's barrier
+    // publishes it.  Otherwise (persist == 0) the workgroup runs its one job.
+    const int queue = blockIdx.x & 7;
+    const int n_static = a.persist >> 3;
+    FA3_LDS int* next = (FA3_LDS int*)(smem + Cfg<D>::kFlagOff + 64);
+    int id = blockIdx.x;
+    for (;;) {
+        KArgs* ap = &kargs();
+        __asm__ volatile("" : "+s"(ap));
+        run(*ap, id);
+        if (a.persist == 0) break;
+        if (threadIdx.x == 0)
+            *next = (int)__hip_atomic_fetch_add(a.queue + kQueueStride * queue, 1u,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unit_gap<2 * (D / 64)>();
+        id = queue + 8 * (*next + n_static);
+        if (id >= a.n_jobs) break;
     }
 }
 
@@ -1435,19 +1511,21 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_component_kernel(FusedArgs a)
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
     int g, pos;
-    job_of(a, g, pos);
+    job_of(kargs(), blockIdx.x, g, pos);
+    // one query head per KV head: group g is head h of batch b
+    const int b = fdiv(kargs().div_hkv, g), h = g - b * a.heads_kv;
     const int QT = a.seqlen / 64;
     if constexpr (kRole == 1) {
-        dkv_role<D, true, false, 1, false, false>(a, g, pos, pos, QT, -1, smem);
+        dkv_role<D, true, false, 1, false, false>(a, kargs(), b, h, pos, pos, QT, -1, smem);
     } else {
         const int qt = QT - 1 - pos;
-        dq_role<D, true, false, 2, false, false>(a, g, qt, 0, qt + 1, -1, smem);
+        dq_role<D, true, false, 2, false, false>(a, kargs(), b, h, h, qt, 0, qt + 1, -1, smem);
     }
 }
 
 template <int D>
 void launch_d(const FusedArgs& a, bool causal, bool bf16, hipStream_t stream) {
-    const dim3 grid(a.n_groups * a.jobs_per_group);
+    const dim3 grid(a.persist > 0 ? a.persist : a.n_groups * a.jobs_per_group);
     const dim3 block(kThreads);
     const bool split = a.bal_m > 0;  // causal only (plan_workspace)
     // K c / Q c cannot overflow fp16 when c <= 1
@@ -1568,6 +1646,22 @@ FusedArgs base_args(const BwdProblem& p, const BwdTensors& t) {
 
 std::atomic<int> g_spin_limit{1 << 24};
 
+// Compute units of the current device (cached per device); 0 if unknown.
+int cu_count() {
+    static std::mutex mu;
+    static int cache[64] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
 // Epochs: a process-wide counter started at a random 64-bit value, so a
 // word left in a workspace by an earlier launch (of this or another
 // process) practically never equals the current launch's epoch.
@@ -1651,6 +1745,8 @@ WorkspacePlan plan_workspace(const BwdProblem& p) {
     at = at.add(rows.mul(sizeof(float)).v).align();
     w.ndelta_off = at.v;
     at = at.add(rows.mul(sizeof(float)).v).align();
+    w.queue_off = at.v;
+    at = at.add(kQueueBytes).align();
     if (!rows.ok) return w;
     // Split plan for causal shapes with one query head per KV head and few
     // jobs (at most two per CU of an MI355X): see bwd_main_kernel.
@@ -1708,8 +1804,9 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     };
     hipError_t err = mark(0);
     if (err != hipSuccess) return err;
-    err = t.packed_in != nullptr ? launch_rowstats(p, t, nlse2, ndelta)
-                                 : launch_preprocess(p, t, nlse2, ndelta);
+    unsigned int* queue = reinterpret_cast<unsigned int*>(ws + plan.queue_off);
+    err = t.packed_in != nullptr ? launch_rowstats(p, t, nlse2, ndelta, queue)
+                                 : launch_preprocess(p, t, nlse2, ndelta, queue);
     if (err == hipSuccess) err = mark(1);
     if (err != hipSuccess) return err;
     a.nlse2 = nlse2;
@@ -1717,6 +1814,13 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     const int group = p.heads_q / p.heads_kv;
     a.jobs_per_group = (p.seqlen / kTileN) * (1 + group);
     set_job_map(a);
+    a.n_jobs = a.n_groups * a.jobs_per_group;
+    a.queue = queue;
+    // persistent default plan once there are at least two jobs per CU: one
+    // workgroup per CU (a multiple of 8, the XCD count) pulls jobs from the
+    // queues, so no CU waits for the in-order dispatch of new workgroups
+    const int cus = cu_count() & ~7;
+    a.persist = plan.bal_m == 0 && cus >= 8 && a.n_jobs >= 2 * cus ? cus : 0;
     a.epoch = next_epoch();
     if (epoch != nullptr) *epoch = a.epoch;
     a.err = reinterpret_cast<unsigned long long*>(ws + plan.err_off);

@@ -21,6 +21,15 @@
 namespace fa3 {
 namespace {
 
+// Zeroes the main kernel's job-queue counters (block 0, one lane per
+// counter; agent-scope stores, as the counters are used by agent-scope
+// atomics).
+__device__ __forceinline__ void clear_queues(unsigned int* queue) {
+    if (queue != nullptr && blockIdx.x == 0 && threadIdx.x < kQueues)
+        __hip_atomic_store(queue + kQueueStride * threadIdx.x, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Rows are [B, Hq, S]; O / dO element strides of one sequence row (q_rs) and
 // one head (q_hs) cover BHSD and BSHD; kBf16: O / dO are bf16.
 template <int D, bool kLse, bool kBf16>
@@ -28,8 +37,9 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const _Float16* __restrict__ dout, const _Float16* __restrict__ out,
     const float* __restrict__ aux0, const float* __restrict__ aux1,
     float* __restrict__ delta, float* __restrict__ nlse2, float* __restrict__ ndelta,
-    float* __restrict__ packed, int rows,
+    float* __restrict__ packed, unsigned int* __restrict__ queue, int rows,
     float scale_log2, int heads_q, int seqlen, int q_rs, int q_hs) {
+    clear_queues(queue);
     constexpr int kLanesPerRow = D / 8;
     constexpr int kRowsPerBlock = 256 / kLanesPerRow;
     const int sub = threadIdx.x % kLanesPerRow;
@@ -65,7 +75,8 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
 }
 
 template <int D>
-hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* nlse2, float* ndelta) {
+hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* nlse2, float* ndelta,
+                        unsigned int* queue) {
     constexpr int kRowsPerBlock = 256 / (D / 8);
     const int rows = p.batch * p.heads_q * p.seqlen;
     const int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
@@ -75,7 +86,7 @@ hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* nlse2, 
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), 0, t.stream, (const _Float16*)t.dout,
                            (const _Float16*)t.out, t.aux0, t.aux1, t.delta, nlse2, ndelta,
-                           t.packed, rows, scale_log2, p.heads_q, p.seqlen,
+                           t.packed, queue, rows, scale_log2, p.heads_q, p.seqlen,
                            q_rs, q_hs);
     };
     if (t.aux_is_lse) {
@@ -94,7 +105,9 @@ hipError_t launch_pre_d(const BwdProblem& p, const BwdTensors& t, float* nlse2, 
 // log2 inv)), and -delta.
 __global__ __launch_bounds__(256) void rowstats_kernel(const float* __restrict__ packed,
                                                        float* __restrict__ nlse2,
-                                                       float* __restrict__ ndelta, int rows) {
+                                                       float* __restrict__ ndelta,
+                                                       unsigned int* __restrict__ queue, int rows) {
+    clear_queues(queue);
     const int r = blockIdx.x * 256 + threadIdx.x;
     if (r >= rows) return;
     nlse2[r] = log2f(packed[(size_t)r * 3 + 1]) - packed[(size_t)r * 3];
@@ -103,17 +116,18 @@ __global__ __launch_bounds__(256) void rowstats_kernel(const float* __restrict__
 
 }  // namespace
 
-hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* nlse2, float* ndelta) {
+hipError_t launch_rowstats(const BwdProblem& p, const BwdTensors& t, float* nlse2, float* ndelta,
+                           unsigned int* queue) {
     const int rows = p.batch * p.heads_q * p.seqlen;
     hipLaunchKernelGGL(rowstats_kernel, dim3((rows + 255) / 256), dim3(256), 0, t.stream,
-                       t.packed_in, nlse2, ndelta, rows);
+                       t.packed_in, nlse2, ndelta, queue, rows);
     return hipGetLastError();
 }
 
 hipError_t launch_preprocess(const BwdProblem& p, const BwdTensors& t, float* nlse2,
-                             float* ndelta) {
-    if (p.head_dim == 128) return launch_pre_d<128>(p, t, nlse2, ndelta);
-    if (p.head_dim == 64) return launch_pre_d<64>(p, t, nlse2, ndelta);
+                             float* ndelta, unsigned int* queue) {
+    if (p.head_dim == 128) return launch_pre_d<128>(p, t, nlse2, ndelta, queue);
+    if (p.head_dim == 64) return launch_pre_d<64>(p, t, nlse2, ndelta, queue);
     return hipErrorInvalidValue;
 }
 

@@ -178,15 +178,19 @@ def row_arrays_bytes(rows):
     return 2 * align(rows * 4)
 
 
+QUEUE_BYTES = 8 * 128  # job-queue counters of the persistent main kernel, one 128-byte line each
+
+
 def plain_bytes(batch, heads_q, seqlen):
-    """Workspace without the split plan: the error word's region and the row
-    arrays."""
-    return ERR_REGION + row_arrays_bytes(batch * heads_q * seqlen)
+    """Workspace without the split plan: the error word's region, the row
+    arrays and the job-queue counters."""
+    return ERR_REGION + row_arrays_bytes(batch * heads_q * seqlen) + QUEUE_BYTES
 
 
 def split_plan_bytes(batch, heads, seqlen, head_dim):
     """Workspace of the split plan (causal, one query head per KV head, at
-    most 512 jobs): the error word's region, lse2 and -delta rows, two
+    most 512 jobs): the error word's region, lse2 and -delta rows, the
+    job-queue counters, two
     64-bit synchronisation words per split job of each role (B*H*QT/2 jobs per
     role), then the fp32 partial sums of one piece per split job -- dK/dV:
     4 waves x 2 matrices x D/64 tiles x 4 KiB, dQ: 4 waves x D/64 tiles x
@@ -194,7 +198,7 @@ def split_plan_bytes(batch, heads, seqlen, head_dim):
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
     rows = batch * heads * seqlen
     jobs = batch * heads * (seqlen // 64 // 2)
-    off = ERR_REGION + row_arrays_bytes(rows)
+    off = ERR_REGION + row_arrays_bytes(rows) + QUEUE_BYTES
     off = align(off + jobs * 4 * 8)
     off = align(off + jobs * 4 * 2 * (head_dim // 64) * 4096)
     return align(off + jobs * 4 * (head_dim // 64) * 4096)
@@ -384,7 +388,7 @@ def test_component_workspace_sizes(lib):
     assert ws5(ctypes.byref(component_params(lib, seqlen=2048, heads_q=4))) == \
         split_plan_bytes(1, 4, 2048, 128)
     p = component_params(lib, heads_q=4, heads_kv=2, causal=False)
-    assert ws5(ctypes.byref(p)) == ERR_REGION + row_arrays_bytes(4 * 256)
+    assert ws5(ctypes.byref(p)) == plain_bytes(1, 4, 256)
     p = component_params(lib)
     p.seqlen_k = 512
     assert ws5(ctypes.byref(p)) == 0
