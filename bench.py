@@ -4,11 +4,15 @@ A step is one full backward through the C ABI over resident fp16 inputs at
 the headline shape B=1, H=4, S=2048, D=128, causal (BASELINE.json
 configs[2]): the delta preprocess and the main kernel, two launches on the
 null stream.  The timed region is `steps` back-to-back shaobo_fa3_bwd_v2
-calls between two HIP events.  Per-kernel durations, back to back: the
-preprocess kernel alone (the same kernel and grid through the
-shaobo_fa3_bwd_dot_do_o component) over as many back-to-back launches
-between two events, and the main kernel as the step minus that; the
-rooflines come from these.  For reference the line also carries the
+calls between two HIP events.  Per-kernel durations, back to back: the main
+kernel alone over as many back-to-back launches between two events
+(shaobo_fa3_ext_bwd_v2_stages with the main-kernel stage, on the workspace
+the timed calls prepared), and the preprocess as the step minus that -- its
+cost inside a step; the rooflines come from these.  The preprocess kernel
+alone in back-to-back launches (the same kernel and grid through the
+shaobo_fa3_bwd_dot_do_o component) is reported beside them: launches of a
+short kernel wait for the host's submissions, so that figure exceeds the
+kernel's share of a step.  For reference the line also carries the
 durations measured by shaobo_fa3_ext_bwd_v2_timed (events recorded before,
 between and after the two kernels of every call), which include each
 marker's dispatch latency and so exceed the kernels' execution times.  Prints one JSON
@@ -242,6 +246,23 @@ def main():
     tflops = f / (ms * 1e-3) / 1e12
 
     # ---- per-kernel durations, back to back ----
+    # the main kernel alone, on the workspace the timed calls left (their
+    # row statistics); the preprocess's share of a step is the rest
+    def main_step():
+        st = lib.shaobo_fa3_ext_bwd_v2_stages(*argv, ctypes.byref(p), None, 2)
+        if st != F.SUCCESS:
+            raise RuntimeError("shaobo_fa3_ext_bwd_v2_stages: " + F.status_name(st))
+
+    for _ in range(5):
+        main_step()
+    torch.cuda.synchronize()
+    hip.record(e0)
+    for _ in range(args.steps):
+        main_step()
+    hip.record(e1)
+    torch.cuda.synchronize()
+    main_ms = hip.elapsed_ms(e0, e1) / args.steps
+    pre_step_ms = ms - main_ms
     # the preprocess alone: the dot_do_o component runs the same kernel on
     # the same rows (delta plus the packed sidecar: the same bytes)
     pp = F.make_params(lib, batch=B, seqlen=S, heads_q=Hq, heads_kv=Hq, head_dim=D,
@@ -263,8 +284,7 @@ def main():
         pre_step()
     hip.record(e1)
     torch.cuda.synchronize()
-    pre_ms = hip.elapsed_ms(e0, e1) / args.steps
-    main_ms = ms - pre_ms
+    pre_alone_ms = hip.elapsed_ms(e0, e1) / args.steps
     # the same number of calls through the timed entry, three events per
     # call, read after one sync (marker-inclusive durations)
     evs = [[hip.event() for _ in range(3)] for _ in range(args.steps)]
@@ -278,7 +298,7 @@ def main():
     main_marked = sum(hip.elapsed_ms(t[1], t[2]) for t in evs) / args.steps
     staged_ms = hip.elapsed_ms(evs[0][0], evs[-1][2]) / args.steps
     main_tflops = f / (main_ms * 1e-3) / 1e12
-    pre_gbs = preprocess_bytes(B, Hq, S, D) / (pre_ms * 1e-3) / 1e9
+    pre_gbs = preprocess_bytes(B, Hq, S, D) / (pre_step_ms * 1e-3) / 1e9
     traffic = load_traffic(args.config)
     result = {
         "metric": METRIC,
@@ -302,7 +322,8 @@ def main():
         "wall_s_timed": round(wall, 4),
         "warmup_steps_run": done,
         "warmup_s": round(warm_s, 3),
-        "kernels_ms": {"preprocess_kernel": round(pre_ms, 5), "bwd_main_kernel": round(main_ms, 5)},
+        "kernels_ms": {"preprocess_kernel": round(pre_step_ms, 5), "bwd_main_kernel": round(main_ms, 5),
+                       "preprocess_alone_back_to_back": round(pre_alone_ms, 5)},
         "kernels_ms_marked": {"preprocess_kernel": round(pre_marked, 5),
                               "bwd_main_kernel": round(main_marked, 5),
                               "ms_per_step": round(staged_ms, 5)},

@@ -146,11 +146,13 @@ int finish(hipError_t err, const ShaoboFa3Params* p, hipStream_t stream = nullpt
 // Options of the extension entries: the launch stream; no_alloc: the
 // library's static scratch array instead of the caller's workspace, whose
 // fields are then ignored; events: three hipEvent_t recorded around the two
-// kernels (or null).
+// kernels (or null); stages: which of the two kernels to launch (bit 0 the
+// preprocess, bit 1 the main kernel).
 struct RunOpts {
     hipStream_t stream = nullptr;
     bool no_alloc = false;
     void* const* events = nullptr;
+    int stages = 3;
 };
 
 // Shared body of v2, the legacy entry and the extension entries.
@@ -196,10 +198,13 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
     if (opt.events != nullptr) {
         for (int i = 0; i < 3; ++i) t.events[i] = static_cast<hipEvent_t>(opt.events[i]);
     }
+    t.stages = opt.stages;
     unsigned long long epoch = 0;
     const hipError_t err = fa3::launch_backward(pr, t, workspace, &epoch);
     const char* ws = static_cast<const char*>(workspace);
-    return finish(err, params, stream, plan.bal_m > 0 ? ws + plan.err_off : nullptr, epoch);
+    // the error word belongs to the main kernel's split waits
+    const bool split = plan.bal_m > 0 && (opt.stages & 2);
+    return finish(err, params, stream, split ? ws + plan.err_off : nullptr, epoch);
 }
 
 // Workspace of v2 and of the legacy entry (the same whatever the aux mode).
@@ -392,6 +397,18 @@ int shaobo_fa3_ext_bwd_v2_timed(const void* dout, const void* q, const void* k, 
     RunOpts opt;
     opt.stream = static_cast<hipStream_t>(stream);
     opt.events = events;
+    return run_backward(dout, q, k, v, out, softmax_lse, nullptr, true, dq, dk, dv, softmax_d,
+                        params, opt);
+}
+
+int shaobo_fa3_ext_bwd_v2_stages(const void* dout, const void* q, const void* k, const void* v,
+                                 const void* out, const void* softmax_lse, void* dq, void* dk,
+                                 void* dv, void* softmax_d, const ShaoboFa3Params* params,
+                                 void* stream, int stages) {
+    if (stages < 1 || stages > 3) return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    RunOpts opt;
+    opt.stream = static_cast<hipStream_t>(stream);
+    opt.stages = stages;
     return run_backward(dout, q, k, v, out, softmax_lse, nullptr, true, dq, dk, dv, softmax_d,
                         params, opt);
 }

@@ -92,6 +92,10 @@ struct BwdTensors {
     // Optional events recorded on `stream` before the preprocess, before the
     // main kernel and after it (null: not recorded).
     hipEvent_t events[3] = {nullptr, nullptr, nullptr};
+    // Kernels to launch: bit 0 the preprocess (or row statistics), bit 1 the
+    // main kernel, which then reads what an earlier preprocess of the same
+    // workspace left there.
+    int stages = 3;
 };
 
 // Device workspace of the v2 / legacy / fused5 entries (regions 256-B

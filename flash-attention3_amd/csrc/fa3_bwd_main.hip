@@ -428,6 +428,13 @@ __device__ __forceinline__ size_t kv_elem(KArgs& a, int b, int h, int s) {
 // ----------------------------------------------------------------------------
 // Outputs
 // ----------------------------------------------------------------------------
+// 16 bytes of a final output (dQ, dK, dV), written with the non-temporal
+// policy: nothing in this launch reads them again, so they stream out
+// instead of sitting dirty in L2 until the kernel's end-of-launch writeback.
+__device__ __forceinline__ void store_out(_Float16* p, f16x8 x) {
+    __builtin_nontemporal_store(x, (f16x8*)p);
+}
+
 // Four consecutive output elements (element offset `off`): the inputs'
 // 16-bit type, or fp32.
 template <bool kBf16>
@@ -525,7 +532,7 @@ __device__ __forceinline__ void store_dkv(KArgs& a, int b, int hkv, int kbase, i
             }
             const f16x8 x = stage_fix(
                 lds_read_b128(st, D == 128 ? stage128_chunk(key, c) : stage64_chunk(key, c)), key);
-            *(f16x8*)(outp + base + (size_t)key * a.kv_rs + d0 + 8 * c) = x;
+            store_out(outp + base + (size_t)key * a.kv_rs + d0 + 8 * c, x);
         }
         return;
     }
@@ -575,7 +582,7 @@ __device__ __forceinline__ void store_dq(KArgs& a, size_t base, int t, int lane,
         for (int j = 0; j < 2 * kRb; ++j) {
             const int r = stage64_row(j, lane), c = lane & 3;  // r: row within the wave's block
             const f16x8 x = stage_fix(lds_read_b128(st, stage64_chunk(r, c)), r);
-            *(f16x8*)(outp + (size_t)(32 * rb0 + r) * a.q_rs + 8 * c) = x;
+            store_out(outp + (size_t)(32 * rb0 + r) * a.q_rs + 8 * c, x);
         }
         return;
     }
@@ -1482,8 +1489,16 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     // gradient waves' last products and epilogue) pops the next id while
     // they finish, and passes it on through LDS; the gap's barrier
     // publishes it.  Otherwise (persist == 0) the workgroup runs its one job.
+    // Queue q serves the n_ids = ceil((n_jobs - q) / 8) ids q, q + 8, ..;
+    // its counter is popped exactly n_ids times in a launch (once per id
+    // beyond the persist / 8 static ones, and once more, unsuccessfully, by
+    // each of its persist / 8 workgroups), so the pop that returns n_ids - 1
+    // is the launch's last on that queue and puts the counter back to 0:
+    // the queues are clean for the next launch even without the
+    // preprocess's clearing.
     const int queue = blockIdx.x & 7;
     const int n_static = a.persist >> 3;
+    const unsigned int n_ids = (unsigned int)(a.n_jobs - queue + 7) >> 3;
     FA3_LDS int* next = (FA3_LDS int*)(smem + Cfg<D>::kFlagOff + 64);
     int id = blockIdx.x;
     for (;;) {
@@ -1491,9 +1506,14 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
         __asm__ volatile("" : "+s"(ap));
         run(*ap, id);
         if (a.persist == 0) break;
-        if (threadIdx.x == 0)
-            *next = (int)__hip_atomic_fetch_add(a.queue + kQueueStride * queue, 1u,
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) {
+            unsigned int* counter = a.queue + kQueueStride * queue;
+            const unsigned int k =
+                __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (k == n_ids - 1)
+                __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *next = (int)k;
+        }
         unit_gap<2 * (D / 64)>();
         id = queue + 8 * (*next + n_static);
         if (id >= a.n_jobs) break;
@@ -1805,10 +1825,13 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     hipError_t err = mark(0);
     if (err != hipSuccess) return err;
     unsigned int* queue = reinterpret_cast<unsigned int*>(ws + plan.queue_off);
-    err = t.packed_in != nullptr ? launch_rowstats(p, t, nlse2, ndelta, queue)
-                                 : launch_preprocess(p, t, nlse2, ndelta, queue);
+    if (t.stages & 1) {
+        err = t.packed_in != nullptr ? launch_rowstats(p, t, nlse2, ndelta, queue)
+                                     : launch_preprocess(p, t, nlse2, ndelta, queue);
+    }
     if (err == hipSuccess) err = mark(1);
     if (err != hipSuccess) return err;
+    if (!(t.stages & 2)) return mark(2);
     a.nlse2 = nlse2;
     a.ndelta = ndelta;
     const int group = p.heads_q / p.heads_kv;

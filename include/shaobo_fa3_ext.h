@@ -63,6 +63,29 @@ int shaobo_fa3_ext_bwd_v2_timed(const void* dout,
                                 void* stream,
                                 void* const* events);
 
+/* shaobo_fa3_bwd_v2_on_stream limited to some of its two kernels: stages
+ * bit 0 launches the delta preprocess, bit 1 the main kernel (3 = both, the
+ * same as shaobo_fa3_bwd_v2_on_stream; anything outside 1..3 returns
+ * SHAOBO_FA3_STATUS_INVALID_VALUE).  No counterpart in the reference; it is
+ * for benchmarks that time one kernel in back-to-back launches (bench.py).
+ * The main kernel alone reads the row statistics the preprocess left in the
+ * workspace, so it needs an earlier call with bit 0 on the same workspace,
+ * inputs and shape, and its dQ / dK / dV then equal those of a full call;
+ * with bit 0 alone only softmax_d and the workspace are written. */
+int shaobo_fa3_ext_bwd_v2_stages(const void* dout,
+                                 const void* q,
+                                 const void* k,
+                                 const void* v,
+                                 const void* out,
+                                 const void* softmax_lse,
+                                 void* dq,
+                                 void* dk,
+                                 void* dv,
+                                 void* softmax_d,
+                                 const ShaoboFa3Params* params,
+                                 void* stream,
+                                 int stages);
+
 /* Size of the device scratch array behind shaobo_fa3_ext_bwd_v2_no_alloc:
  * 32 MiB per GPU, held from the library's first use on that GPU until the
  * process ends. */

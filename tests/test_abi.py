@@ -279,6 +279,14 @@ def test_launch_error_paths_without_gpu(lib):
     p = supported(lib)
     assert lib.shaobo_fa3_bwd_dot_do_o(one, one, one, None, one, None,
                                        ctypes.byref(p)) == F.INVALID_VALUE
+    # stage-selecting extension: a stage mask outside 1..3 is refused first,
+    # then the v2 checks apply
+    p = supported(lib)
+    for stages in (0, 4, -1):
+        assert lib.shaobo_fa3_ext_bwd_v2_stages(*args, ctypes.byref(p), None,
+                                                stages) == F.INVALID_VALUE
+    p.batch = 0
+    assert lib.shaobo_fa3_ext_bwd_v2_stages(*args, ctypes.byref(p), None, 2) == F.INVALID_VALUE
 
 
 def random_params(rng, p):
