@@ -416,12 +416,12 @@ __device__ __forceinline__ f16x8 swap_halves(f16x8 x) {
     return __builtin_bit_cast(f16x8, u64x2{lo, hi});
 }
 // Element offset of sequence row s of head h in batch b.
-template <int D>
-__device__ __forceinline__ size_t q_elem(KArgs& a, int b, int h, int s) {
+template <int D, typename A>
+__device__ __forceinline__ size_t q_elem(const A& a, int b, int h, int s) {
     return (size_t)b * a.heads_q * a.seqlen * D + (size_t)h * a.q_hs + (size_t)s * a.q_rs;
 }
-template <int D>
-__device__ __forceinline__ size_t kv_elem(KArgs& a, int b, int h, int s) {
+template <int D, typename A>
+__device__ __forceinline__ size_t kv_elem(const A& a, int b, int h, int s) {
     return (size_t)b * a.heads_kv * a.seqlen * D + (size_t)h * a.kv_hs + (size_t)s * a.kv_rs;
 }
 
@@ -437,8 +437,8 @@ __device__ __forceinline__ void store_out(_Float16* p, f16x8 x) {
 
 // Four consecutive output elements (element offset `off`): the inputs'
 // 16-bit type, or fp32.
-template <bool kBf16>
-__device__ __forceinline__ void store4(KArgs& a, void* base, size_t off, f32x4 v) {
+template <bool kBf16, typename A>
+__device__ __forceinline__ void store4(const A& a, void* base, size_t off, f32x4 v) {
     if (a.out_f32) {
         *(f32x4*)((float*)base + off) = v;
     } else {
@@ -494,8 +494,8 @@ __device__ __forceinline__ int stage64_row(int j, int lane) {
 // and cover D columns d0 .. d0 + 32 kPpw of all 64 keys; 16-bit outputs are
 // transposed through the wave's own 8 KiB (D 64: 4 KiB) of `stage` so that
 // every global store writes whole 128-byte (D 64: 64-byte) row segments.
-template <int D, bool kBf16>
-__device__ __forceinline__ void store_dkv(KArgs& a, int b, int hkv, int kbase, int t, int lane,
+template <int D, bool kBf16, typename A>
+__device__ __forceinline__ void store_dkv(const A& a, int b, int hkv, int kbase, int t, int lane,
                                           const f32x16 (&acc)[D / 64][2], FA3_LDS char* stage) {
     constexpr int kPpw = D / 64;
     const int l32 = lane & 31, h = lane >> 5;
@@ -559,8 +559,8 @@ __device__ __forceinline__ void store_dkv(KArgs& a, int b, int hkv, int kbase, i
 // lane: row 32 rb + l32, d = 32 db + 8 (i / 4) + 4 h + i % 4.  16-bit
 // outputs go through the wave's 4 KiB (D 64: 2 KiB) of `stage`, so every
 // global store writes whole 64-byte row segments.
-template <int D, bool kBf16>
-__device__ __forceinline__ void store_dq(KArgs& a, size_t base, int t, int lane,
+template <int D, bool kBf16, typename A>
+__device__ __forceinline__ void store_dq(const A& a, size_t base, int t, int lane,
                                          const f32x16 (&acc)[D / 64], FA3_LDS char* stage) {
     constexpr int kRb = D / 64;
     const int db = D == 128 ? t : t >> 1;
@@ -732,8 +732,8 @@ __device__ __forceinline__ bool split_end(const A& a, int job, FA3_LDS int* flag
 // the job is whole and writes dK / dV; otherwise the unit is piece slot & 1
 // of split job slot >> 1 and the pieces' partial sums meet in split_end.
 template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false,
-          bool kScaled = true>
-__device__ __forceinline__ void dkv_role(const FusedArgs& a, KArgs& d, int b, int hkv, int kt, int qa, int qb,
+          bool kScaled = true, typename DA>
+__device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b, int hkv, int kt, int qa, int qb,
                                          int slot,
                          FA3_LDS char* smem) {
     static_assert(kRows == 0 || kRows == 1, "dKV rows come as -lse2/-delta or packed");
@@ -1087,8 +1087,8 @@ __device__ __forceinline__ void dkv_role(const FusedArgs& a, KArgs& d, int b, in
 // tiles [ka, kb) (the causal diagonal, key tile qt, is masked).  slot: as
 // for dkv_role.
 template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false,
-          bool kScaled = true>
-__device__ __forceinline__ void dq_role(const FusedArgs& a, KArgs& d, int b, int hq, int hkv, int qt, int ka,
+          bool kScaled = true, typename DA>
+__device__ __forceinline__ void dq_role(const FusedArgs& a, const DA& d, int b, int hq, int hkv, int qt, int ka,
                                         int kb, int slot,
                         FA3_LDS char* smem) {
     static_assert(kRows == 0 || kRows == 2, "dQ rows come as -lse2/-delta or max/sum/delta");
@@ -1376,7 +1376,8 @@ __device__ __forceinline__ void unit_gap() {
 }
 
 // Job id -> (group, position in the group); see the job map below.
-__device__ __forceinline__ void job_of(KArgs& a, int id, int& g, int& pos) {
+template <typename A>
+__device__ __forceinline__ void job_of(const A& a, int id, int& g, int& pos) {
     if (a.xcd_parts > 0) {
         const int xcd = id & 7;
         const int n = id >> 3;
@@ -1433,38 +1434,38 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     const int QT = a.seqlen / 64;
     int g, pos;
     if constexpr (kSplit) {
-        job_of(kargs(), blockIdx.x, g, pos);
+        job_of(a, blockIdx.x, g, pos);
         // G = 1: group g is query head g (and KV head g) of batch b
-        const int b = fdiv(kargs().div_hkv, g), h = g - b * a.heads_kv;
+        const int b = fdiv(a.div_hkv, g), h = g - b * a.heads_kv;
         const int M = a.bal_m;
         const int job0 = g * M;
         if (pos < M) {
             // dKV key tile M + x whole, then the remainder of dQ query tile M + x
             const int x = pos, nq = M + x + 1, lq = a.head_q[x];
-            dkv_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, M + x, M + x, QT, -1, smem);
+            dkv_role<D, kCausal, kBf16, 0, true, false>(a, a, b, h, M + x, M + x, QT, -1, smem);
             if (lq < nq) {
                 unit_gap<4 * (D / 64)>();
-                dq_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, h, M + x, lq, nq,
+                dq_role<D, kCausal, kBf16, 0, true, false>(a, a, b, h, h, M + x, lq, nq,
                                                         2 * (job0 + x) + 1, smem);
             }
         } else if (pos < 2 * M) {
             // dQ query tile x whole, then the remainder of dKV key tile x
             const int x = pos - M, nkv = QT - x, lkv = a.head_kv[x];
-            dq_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, h, x, 0, x + 1, -1, smem);
+            dq_role<D, kCausal, kBf16, 0, true, false>(a, a, b, h, h, x, 0, x + 1, -1, smem);
             if (lkv < nkv) {
                 unit_gap<2 * (D / 64)>();
-                dkv_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, x, x + lkv, QT,
+                dkv_role<D, kCausal, kBf16, 0, true, false>(a, a, b, h, x, x + lkv, QT,
                                                          2 * (job0 + x) + 1, smem);
             }
         } else if (pos < 3 * M) {
             // head piece (or all) of dKV key tile x
             const int x = pos - 2 * M, nkv = QT - x, lkv = a.head_kv[x];
-            dkv_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, x, x, x + min(lkv, nkv),
+            dkv_role<D, kCausal, kBf16, 0, true, false>(a, a, b, h, x, x, x + min(lkv, nkv),
                                                      lkv < nkv ? 2 * (job0 + x) : -1, smem);
         } else {
             // head piece (or all) of dQ query tile M + x
             const int x = pos - 3 * M, nq = M + x + 1, lq = a.head_q[x];
-            dq_role<D, kCausal, kBf16, 0, true, false>(a, kargs(), b, h, h, M + x, 0, min(lq, nq),
+            dq_role<D, kCausal, kBf16, 0, true, false>(a, a, b, h, h, M + x, 0, min(lq, nq),
                                                     lq < nq ? 2 * (job0 + x) : -1, smem);
         }
         return;
@@ -1531,15 +1532,15 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_component_kernel(FusedArgs a)
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
     int g, pos;
-    job_of(kargs(), blockIdx.x, g, pos);
+    job_of(a, blockIdx.x, g, pos);
     // one query head per KV head: group g is head h of batch b
-    const int b = fdiv(kargs().div_hkv, g), h = g - b * a.heads_kv;
+    const int b = fdiv(a.div_hkv, g), h = g - b * a.heads_kv;
     const int QT = a.seqlen / 64;
     if constexpr (kRole == 1) {
-        dkv_role<D, true, false, 1, false, false>(a, kargs(), b, h, pos, pos, QT, -1, smem);
+        dkv_role<D, true, false, 1, false, false>(a, a, b, h, pos, pos, QT, -1, smem);
     } else {
         const int qt = QT - 1 - pos;
-        dq_role<D, true, false, 2, false, false>(a, kargs(), b, h, h, qt, 0, qt + 1, -1, smem);
+        dq_role<D, true, false, 2, false, false>(a, a, b, h, h, qt, 0, qt + 1, -1, smem);
     }
 }
 
