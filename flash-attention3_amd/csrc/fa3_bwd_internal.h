@@ -16,10 +16,12 @@ constexpr int kTileN = 64;
 constexpr int kTileM = 64;
 
 // Job queues of the persistent main kernel: one counter per XCD (workgroup
-// id % 8), each on its own 128-byte line of the workspace, zeroed by the
-// preprocess pass that runs before the main kernel.
+// id % 8), each on its own 128-byte line of the workspace, and an exit
+// count; zeroed by the preprocess pass that runs before the main kernel
+// (and by the main kernel's last workgroup as it leaves).
 constexpr int kQueues = 8;
 constexpr int kQueueStride = 32;  // 32-bit words between counters
+constexpr int kQueueExitWord = 16;  // the launch's exit count, on queue 0's line
 constexpr size_t kQueueBytes = (size_t)kQueues * kQueueStride * 4;
 
 // Division by a launch-invariant divisor d (1 <= d < 2^31) of 0 <= n < 2^31

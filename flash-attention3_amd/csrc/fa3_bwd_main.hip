@@ -1490,34 +1490,50 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     // gradient waves' last products and epilogue) pops the next id while
     // they finish, and passes it on through LDS; the gap's barrier
     // publishes it.  Otherwise (persist == 0) the workgroup runs its one job.
-    // Queue q serves the n_ids = ceil((n_jobs - q) / 8) ids q, q + 8, ..;
-    // its counter is popped exactly n_ids times in a launch (once per id
-    // beyond the persist / 8 static ones, and once more, unsuccessfully, by
-    // each of its persist / 8 workgroups), so the pop that returns n_ids - 1
-    // is the launch's last on that queue and puts the counter back to 0:
-    // the queues are clean for the next launch even without the
-    // preprocess's clearing.
-    const int queue = blockIdx.x & 7;
+    // Queue q holds the ids q + 8 (k + persist / 8), k = 0, 1, .. below
+    // n_jobs (its first persist / 8 ids are the static first jobs of the
+    // workgroups q, q + 8, ..).  A workgroup drains its own XCD's queue,
+    // then steals from the others in turn (the XCDs do not run at one speed:
+    // 7 % apart at P4, 17 % at P5 without stealing), and leaves when every
+    // queue is dry.  Every id below n_jobs is popped once.  The last
+    // workgroup to leave (the exit count, kept on queue 0's line) puts all
+    // counters back to 0, so the queues are clean for the next launch even
+    // without the preprocess's clearing.
     const int n_static = a.persist >> 3;
-    const unsigned int n_ids = (unsigned int)(a.n_jobs - queue + 7) >> 3;
+    int qcur = blockIdx.x & 7;  // thread 0: the queue being drained
     FA3_LDS int* next = (FA3_LDS int*)(smem + Cfg<D>::kFlagOff + 64);
     int id = blockIdx.x;
     for (;;) {
         KArgs* ap = &kargs();
         __asm__ volatile("" : "+s"(ap));
         run(*ap, id);
-        if (a.persist == 0) break;
+        if (a.persist == 0) return;
         if (threadIdx.x == 0) {
-            unsigned int* counter = a.queue + kQueueStride * queue;
-            const unsigned int k =
-                __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (k == n_ids - 1)
-                __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *next = (int)k;
+            int nid = -1;
+            for (int tries = 0; tries < kQueues && nid < 0; ++tries) {
+                const unsigned int k = __hip_atomic_fetch_add(a.queue + kQueueStride * qcur, 1u,
+                                                              __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT);
+                const long long cand = qcur + 8 * ((long long)k + n_static);
+                if (cand < a.n_jobs) nid = (int)cand;
+                else qcur = (qcur + 1) & 7;
+            }
+            *next = nid;
         }
         unit_gap<2 * (D / 64)>();
-        id = queue + 8 * (*next + n_static);
-        if (id >= a.n_jobs) break;
+        id = *next;
+        if (id < 0) break;
+    }
+    if (threadIdx.x == 0) {
+        // every pop of this workgroup has returned before its exit counts
+        unsigned int* exits = a.queue + kQueueExitWord;
+        if (__hip_atomic_fetch_add(exits, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            (unsigned int)a.persist - 1) {
+            for (int q = 0; q < kQueues; ++q)
+                __hip_atomic_store(a.queue + kQueueStride * q, 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(exits, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 

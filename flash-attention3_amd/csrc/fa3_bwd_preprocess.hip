@@ -21,13 +21,14 @@
 namespace fa3 {
 namespace {
 
-// Zeroes the main kernel's job-queue counters (block 0, one lane per
-// counter; agent-scope stores, as the counters are used by agent-scope
+// Zeroes the main kernel's job-queue counters and exit count (block 0, one
+// lane per word; agent-scope stores, as the words are used by agent-scope
 // atomics).
 __device__ __forceinline__ void clear_queues(unsigned int* queue) {
-    if (queue != nullptr && blockIdx.x == 0 && threadIdx.x < kQueues)
-        __hip_atomic_store(queue + kQueueStride * threadIdx.x, 0u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+    if (queue != nullptr && blockIdx.x == 0 && threadIdx.x <= kQueues)
+        __hip_atomic_store(queue + (threadIdx.x < kQueues ? kQueueStride * threadIdx.x
+                                                           : kQueueExitWord),
+                           0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Rows are [B, Hq, S]; O / dO element strides of one sequence row (q_rs) and
