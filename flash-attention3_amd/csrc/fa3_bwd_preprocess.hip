@@ -47,20 +47,29 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
     if (row >= rows) return;  // rows % kRowsPerBlock may be non-zero only at the tail
 
-    const int hs = heads_q * seqlen;
-    const int b = row / hs, rem = row - b * hs, h = rem / seqlen, sq = rem - h * seqlen;
-    const size_t elem = (size_t)b * hs * D + (size_t)h * q_hs + (size_t)sq * q_rs;
+    // The row's statistics are loaded by every lane of the row, beside its
+    // O / dO loads, so the kernel waits out one memory round trip, not two.
+    const float a0 = aux0[row];
+    const float a1 = kLse ? 0.f : aux1[row];
+    size_t elem;
+    if (q_rs == D && q_hs == seqlen * D) {
+        elem = (size_t)row * D;  // BHSD: O / dO rows in the order of the statistics rows
+    } else {
+        const int hs = heads_q * seqlen;
+        const int b = row / hs, rem = row - b * hs, h = rem / seqlen, sq = rem - h * seqlen;
+        elem = (size_t)b * hs * D + (size_t)h * q_hs + (size_t)sq * q_rs;
+    }
     const float acc = row_delta<D, kBf16>(dout, out, elem, sub);
 
     if (sub == 0) {
         float l2, max_log2, inv_sum;
         if constexpr (kLse) {
-            l2 = aux0[row] * kLog2e;
+            l2 = a0 * kLog2e;
             max_log2 = l2;
             inv_sum = 1.f;
         } else {
-            const float s = aux1[row];
-            max_log2 = aux0[row] * scale_log2;
+            const float s = a1;
+            max_log2 = a0 * scale_log2;
             inv_sum = s != 0.f ? 1.f / s : 0.f;
             l2 = max_log2 + log2f(s);
         }
