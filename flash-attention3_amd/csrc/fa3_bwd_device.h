@@ -64,6 +64,13 @@ __device__ __forceinline__ int p1_chunk(int s, int g4) {
     else return s + 2 * (g4 >> 1) + 4 * (g4 & 1);
 }
 
+// x of the lane that DPP control kCtrl selects (all rows and banks enabled).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), kCtrl, 0xF, 0xF, false));
+}
+
 // delta = sum_d fp32(dO[row, d]) * fp32(O[row, d]) of one query row whose
 // elements start at `elem`: lane `sub` of the row's D / 8 consecutive lanes
 // takes the 16-byte chunk sub (dot8), then a butterfly over those lanes.
@@ -72,8 +79,21 @@ __device__ __forceinline__ float row_delta(const _Float16* dout, const _Float16*
                                            int sub) {
     const size_t c = elem + (size_t)sub * 8;
     float acc = dot8<kBf16>(*(const f16x8*)(dout + c), *(const f16x8*)(out + c), 0.f);
+    if constexpr (D == 128) {
+        // The row's 16 lanes are one DPP row: the butterfly's partners at
+        // distance 8, 4, 2, 1 through row_ror:8, row_ror:4 and two quad
+        // permutations instead of four LDS-crossbar shuffles.  After the
+        // first step a lane's value depends on lane % 8 only, so the lane 4
+        // places round the row holds the same value as the lane at xor 4:
+        // the same sums in the same order.
+        acc += dpp_f32<0x128>(acc);  // row_ror:8
+        acc += dpp_f32<0x124>(acc);  // row_ror:4
+        acc += dpp_f32<0x4E>(acc);   // quad_perm [2, 3, 0, 1]
+        acc += dpp_f32<0xB1>(acc);   // quad_perm [1, 0, 3, 2]
+    } else {
 #pragma unroll
-    for (int off = D / 16; off > 0; off >>= 1) acc += __shfl_xor(acc, off, D / 8);
+        for (int off = D / 16; off > 0; off >>= 1) acc += __shfl_xor(acc, off, D / 8);
+    }
     return acc;
 }
 
