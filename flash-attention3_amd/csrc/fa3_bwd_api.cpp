@@ -23,6 +23,22 @@
 
 #include "fa3_bwd_internal.h"
 
+namespace fa3 {
+hipError_t launch_device(hipStream_t stream, int* dev) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (stream != nullptr) {
+        hipDevice_t sd = -1;
+        e = hipStreamGetDevice(stream, &sd);
+        if (e != hipSuccess) return e;
+        if ((int)sd != cur) return hipErrorInvalidDevice;
+    }
+    *dev = cur;
+    return hipSuccess;
+}
+}  // namespace fa3
+
 // The struct layout is part of the ABI: pin it (reference header order,
 // x86-64 SysV offsets).
 static_assert(offsetof(ShaoboFa3Params, struct_size) == 0, "abi");
@@ -125,22 +141,39 @@ fa3::BwdProblem problem_of(const ShaoboFa3Params* p) {
 // behaviour), the caller's stream otherwise.  When the launch used the split
 // plan, the synchronised call also reads the workspace's error word: a split
 // wait that gave up wrote the launch's epoch there, and the call reports a
-// HIP error instead of returning wrong gradients as success.
+// HIP error instead of returning wrong gradients as success.  On a caller's
+// stream the word is read by a copy queued on that stream, so the one
+// stream synchronisation covers it (no other stream is waited for).
 int finish(hipError_t err, const ShaoboFa3Params* p, hipStream_t stream = nullptr,
            const void* err_word = nullptr, unsigned long long epoch = 0) {
     if (err != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
-    if (p->sync_after_launch) {
-        const hipError_t e = stream == nullptr ? hipDeviceSynchronize() : hipStreamSynchronize(stream);
-        if (e != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
-        if (err_word != nullptr) {
-            unsigned long long word = 0;
-            if (hipMemcpy(&word, err_word, sizeof(word), hipMemcpyDeviceToHost) != hipSuccess ||
-                word == epoch) {
-                return SHAOBO_FA3_STATUS_HIP_ERROR;
-            }
+    if (!p->sync_after_launch) return SHAOBO_FA3_STATUS_SUCCESS;
+    unsigned long long word = 0;
+    if (stream == nullptr) {
+        if (hipDeviceSynchronize() != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
+        if (err_word != nullptr &&
+            hipMemcpy(&word, err_word, sizeof(word), hipMemcpyDeviceToHost) != hipSuccess) {
+            return SHAOBO_FA3_STATUS_HIP_ERROR;
         }
+    } else {
+        if (err_word != nullptr && hipMemcpyAsync(&word, err_word, sizeof(word),
+                                                  hipMemcpyDeviceToHost, stream) != hipSuccess) {
+            return SHAOBO_FA3_STATUS_HIP_ERROR;
+        }
+        if (hipStreamSynchronize(stream) != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
     }
+    if (err_word != nullptr && word == epoch) return SHAOBO_FA3_STATUS_HIP_ERROR;
     return SHAOBO_FA3_STATUS_SUCCESS;
+}
+
+// Device of the launches on `stream`: SUCCESS, INVALID_VALUE for a stream
+// of another device than the current one (the library's per-device arrays
+// are looked up with the launch device current), HIP_ERROR when the runtime
+// fails.
+int resolve_device(hipStream_t stream, int* dev) {
+    const hipError_t e = fa3::launch_device(stream, dev);
+    if (e == hipErrorInvalidDevice) return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    return e == hipSuccess ? SHAOBO_FA3_STATUS_SUCCESS : SHAOBO_FA3_STATUS_HIP_ERROR;
 }
 
 // Options of the extension entries: the launch stream; no_alloc: the
@@ -177,11 +210,17 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
         if (!plan.ok || plan.total > fa3::kNoAllocScratchBytes) {
             return SHAOBO_FA3_STATUS_INVALID_VALUE;
         }
-        if (fa3::noalloc_scratch(&workspace) != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
     } else if (!plan.ok || workspace == nullptr || params->workspace_bytes < plan.total) {
         return SHAOBO_FA3_STATUS_INVALID_VALUE;
     }
+    int device = -1;
+    const int dev_status = resolve_device(stream, &device);
+    if (dev_status != SHAOBO_FA3_STATUS_SUCCESS) return dev_status;
+    if (opt.no_alloc && fa3::noalloc_scratch(device, &workspace) != hipSuccess) {
+        return SHAOBO_FA3_STATUS_HIP_ERROR;
+    }
     fa3::BwdTensors t;
+    t.device = device;
     t.dout = dout;
     t.q = q;
     t.k = k;
@@ -379,6 +418,8 @@ int shaobo_fa3_bwd_v2_on_stream(const void* dout, const void* q, const void* k, 
 
 void shaobo_fa3_ext_set_split_spin_limit(int polls) { fa3::set_split_spin_limit(polls); }
 
+void shaobo_fa3_ext_set_race_check(int on) { fa3::set_debug_kernels(on != 0); }
+
 int shaobo_fa3_ext_bwd_v2_no_alloc(const void* dout, const void* q, const void* k, const void* v,
                                    const void* out, const void* softmax_lse, void* dq, void* dk,
                                    void* dv, void* softmax_d, const ShaoboFa3Params* params,
@@ -411,6 +452,51 @@ int shaobo_fa3_ext_bwd_v2_stages(const void* dout, const void* q, const void* k,
     opt.stages = stages;
     return run_backward(dout, q, k, v, out, softmax_lse, nullptr, true, dq, dk, dv, softmax_d,
                         params, opt);
+}
+
+int shaobo_fa3_ext_split_status(const void* workspace, void* stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int device = -1;
+    const int dev_status = resolve_device(s, &device);
+    if (dev_status != SHAOBO_FA3_STATUS_SUCCESS) return dev_status;
+    const char* base = static_cast<const char*>(workspace);
+    if (base == nullptr) {
+        void* p = nullptr;
+        if (fa3::noalloc_scratch(device, &p) != hipSuccess) return SHAOBO_FA3_STATUS_HIP_ERROR;
+        base = static_cast<const char*>(p);
+    }
+    void* word_ptr = const_cast<char*>(base + fa3::kErrWordOffset);
+    unsigned long long word = 0;
+    if (hipMemcpyAsync(&word, word_ptr, sizeof(word), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        return SHAOBO_FA3_STATUS_HIP_ERROR;
+    }
+    if (!fa3::epoch_issued(word)) return SHAOBO_FA3_STATUS_SUCCESS;
+    // reported once: the word goes back to 0 (no launch uses epoch 0)
+    if (hipMemsetAsync(word_ptr, 0, sizeof(word), s) != hipSuccess) {
+        return SHAOBO_FA3_STATUS_HIP_ERROR;
+    }
+    (void)hipStreamSynchronize(s);
+    return SHAOBO_FA3_STATUS_HIP_ERROR;
+}
+
+int shaobo_fa3_ext_split_error_count(void* stream, unsigned long long* count) {
+    if (count == nullptr) return SHAOBO_FA3_STATUS_INVALID_VALUE;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int device = -1;
+    const int dev_status = resolve_device(s, &device);
+    if (dev_status != SHAOBO_FA3_STATUS_SUCCESS) return dev_status;
+    unsigned long long* counter = nullptr;
+    if (fa3::split_giveup_count(device, &counter) != hipSuccess) {
+        return SHAOBO_FA3_STATUS_HIP_ERROR;
+    }
+    unsigned long long n = 0;
+    if (hipMemcpyAsync(&n, counter, sizeof(n), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        return SHAOBO_FA3_STATUS_HIP_ERROR;
+    }
+    *count = n;
+    return SHAOBO_FA3_STATUS_SUCCESS;
 }
 
 const char* shaobo_fa3_status_string(int status) {
@@ -507,6 +593,8 @@ int shaobo_fa3_bwd_fused5(const void* dout, const void* q, const void* k, const 
     if (!plan.ok || params->workspace == nullptr || params->workspace_bytes < plan.total) {
         return SHAOBO_FA3_STATUS_INVALID_VALUE;
     }
+    const int dev_status = resolve_device(nullptr, &t.device);
+    if (dev_status != SHAOBO_FA3_STATUS_SUCCESS) return dev_status;
     unsigned long long epoch = 0;
     const hipError_t err = fa3::launch_backward(pr, t, params->workspace, &epoch);
     const char* ws = static_cast<const char*>(params->workspace);

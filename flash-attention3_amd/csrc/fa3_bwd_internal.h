@@ -89,8 +89,10 @@ struct BwdTensors {
     const float* packed_in = nullptr;
     const float* delta_in = nullptr;
     // Stream of every launch (null: the legacy default stream, as in the
-    // reference ABI; the stream entry points pass the caller's).
+    // reference ABI; the stream entry points pass the caller's) and its
+    // device, which is the current device (launch_device).
     hipStream_t stream = nullptr;
+    int device = -1;
     // Optional events recorded on `stream` before the preprocess, before the
     // main kernel and after it (null: not recorded).
     hipEvent_t events[3] = {nullptr, nullptr, nullptr};
@@ -157,10 +159,34 @@ hipError_t launch_naive(const BwdProblem& p, const BwdTensors& t, void* workspac
 // Polls a split wait makes before it gives up (test hook; default 1 << 24).
 void set_split_spin_limit(int polls);
 
+// Race-check instantiations of the main kernel for the launches that follow
+// (test hook; see shaobo_fa3_ext_set_race_check).
+void set_debug_kernels(bool on);
+
+// Device of the launches on `stream` (null: the legacy default stream of
+// the current device).  The library's per-device arrays (the no-allocation
+// scratch, the give-up count) are looked up with that device current, so a
+// stream of another device than the current one is refused
+// (hipErrorInvalidDevice).
+hipError_t launch_device(hipStream_t stream, int* dev);
+
 // Workspace of the no-allocation entry: a static device array of
 // kNoAllocScratchBytes per GPU.  noalloc_scratch returns its device address
-// on the current device (looked up once per device, then cached).
+// on device dev, which must be current (looked up once per device, then
+// cached).
 constexpr size_t kNoAllocScratchBytes = SHAOBO_FA3_EXT_SCRATCH_BYTES;
-hipError_t noalloc_scratch(void** ptr);
+hipError_t noalloc_scratch(int dev, void** ptr);
+
+// Device address of device dev's count of split waits that gave up (a
+// 64-bit counter the kernels increment; dev must be current).
+hipError_t split_giveup_count(int dev, unsigned long long** ptr);
+
+// Whether `word` is an epoch one of this process's launches used: an error
+// word holding one was written by a split wait that gave up (garbage in an
+// uninitialised workspace practically never falls in that range).
+bool epoch_issued(unsigned long long word);
+
+// Byte offset of the error word in every v2 / legacy / fused5 workspace.
+constexpr size_t kErrWordOffset = 0;
 
 }  // namespace fa3

@@ -35,7 +35,8 @@ EXPORTS = (
     "shaobo_fa3_bwd_dq_workspace_bytes", "shaobo_fa3_bwd_dq",
     "shaobo_fa3_bwd_v2_on_stream", "shaobo_fa3_ext_set_split_spin_limit",
     "shaobo_fa3_ext_bwd_v2_no_alloc", "shaobo_fa3_ext_bwd_v2_timed",
-    "shaobo_fa3_ext_bwd_v2_stages",
+    "shaobo_fa3_ext_bwd_v2_stages", "shaobo_fa3_ext_split_status",
+    "shaobo_fa3_ext_split_error_count",
 )
 
 # Size of the static device scratch array behind shaobo_fa3_ext_bwd_v2_no_alloc
@@ -160,6 +161,11 @@ def load(path=LIB_PATH):
         lib.shaobo_fa3_ext_bwd_v2_stages.argtypes = [ctypes.c_void_p] * 10 + [
             ctypes.POINTER(Params), ctypes.c_void_p, ctypes.c_int]
         lib.shaobo_fa3_ext_bwd_v2_stages.restype = ctypes.c_int
+        lib.shaobo_fa3_ext_split_status.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        lib.shaobo_fa3_ext_split_status.restype = ctypes.c_int
+        lib.shaobo_fa3_ext_split_error_count.argtypes = [
+            ctypes.c_void_p, ctypes.POINTER(ctypes.c_ulonglong)]
+        lib.shaobo_fa3_ext_split_error_count.restype = ctypes.c_int
         if path != LIB_PATH:
             return lib
         _LIB = lib

@@ -9,6 +9,11 @@ stream through the library's stream entry point
 correctly with the surrounding torch work and with CUDA-graph capture of
 that stream.  A fake (meta) implementation gives shapes for tracing.
 
+The op launches without synchronising, so a split wait that gave up (the
+library's bounded wait between two workgroups sharing one output tile) cannot
+fail the call itself; ``check_split_errors`` is the op's synchronisation
+point that reports it (through shaobo_fa3_ext_split_error_count).
+
 ``attention`` wraps it in an autograd function whose forward is a plain
 torch computation (O and the natural-log LSE in fp32, O rounded to the inputs' dtype) --
 an integration example and a test vehicle; the library provides the
@@ -88,6 +93,30 @@ def flash_attn_backward(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v:
     if st != F.SUCCESS:
         raise RuntimeError("shaobo_fa3_bwd_v2_on_stream: " + F.status_name(st))
     return dq, dk, dv, delta
+
+
+_SPLIT_ERRORS_SEEN = {}
+
+
+def check_split_errors(device=None):
+    """Synchronise torch's current stream on `device` and raise RuntimeError
+    if a split wait of the library gave up on that GPU since the previous
+    check (those launches returned wrong gradients).  Call it where the
+    caller synchronises anyway (end of a step, before reading a loss)."""
+    lib = _lib()
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None \
+        else torch.device(device)
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        n = ctypes.c_ulonglong(0)
+        st = lib.shaobo_fa3_ext_split_error_count(ctypes.c_void_p(stream), ctypes.byref(n))
+    if st != F.SUCCESS:
+        raise RuntimeError("shaobo_fa3_ext_split_error_count: " + F.status_name(st))
+    seen = _SPLIT_ERRORS_SEEN.get(dev.index, 0)
+    _SPLIT_ERRORS_SEEN[dev.index] = n.value
+    if n.value != seen:
+        raise RuntimeError(f"shaobo_fa3: {n.value - seen} split wait(s) gave up on {dev}: "
+                           "the gradients of those backward calls are wrong")
 
 
 @flash_attn_backward.register_fake

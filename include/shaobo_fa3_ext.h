@@ -18,7 +18,9 @@ extern "C" {
  * torch.cuda.current_stream()).  `stream` is a hipStream_t (NULL = the null
  * stream, which makes this identical to shaobo_fa3_bwd_v2).  Validation,
  * statuses, workspace and outputs are those of shaobo_fa3_bwd_v2;
- * sync_after_launch synchronises `stream` (the device for NULL).  The
+ * sync_after_launch synchronises `stream` (the device for NULL).  A stream
+ * of another GPU than the current one returns
+ * SHAOBO_FA3_STATUS_INVALID_VALUE (make its GPU current first).  The
  * workspace must not be shared by calls that may run concurrently. */
 int shaobo_fa3_bwd_v2_on_stream(const void* dout,
                                 const void* q,
@@ -38,10 +40,47 @@ int shaobo_fa3_bwd_v2_on_stream(const void* dout,
  * before it gives up (default 1 << 24, each poll followed by a short sleep).
  * A wait that gives up still finishes its workgroup normally, writes the
  * launch's epoch into the workspace's error word and the synchronised call
- * (sync_after_launch = 1) returns SHAOBO_FA3_STATUS_HIP_ERROR; 0 makes every
+ * (sync_after_launch = 1) returns SHAOBO_FA3_STATUS_HIP_ERROR (unsynchronised
+ * calls: shaobo_fa3_ext_split_status / _split_error_count); 0 makes every
  * split wait give up at once.  Process-wide; affects launches made after the
  * call. */
 void shaobo_fa3_ext_set_split_spin_limit(int polls);
+
+/* Test hook, no counterpart in the reference: with on != 0 the launches
+ * that follow (v2, its stream / timed / stages / no-allocation variants,
+ * the legacy entry, fused5) run the race-check instantiation of the main
+ * kernel.  It does the same arithmetic in the same order as the fast kernel
+ * with the pipeline's concurrency taken out: every job starts on an LDS
+ * filled with 0xFF bytes (a NaN in fp16, bf16 and fp32, so a read of LDS
+ * the job did not write shows in its outputs), and after each LDS phase of
+ * a pipeline step every wave waits for all its memory operations and meets
+ * the others at a barrier.  Its outputs must equal the fast kernel's bit
+ * for bit; it is several times slower.  0 restores the fast kernel.
+ * Process-wide. */
+void shaobo_fa3_ext_set_race_check(int on);
+
+/* Whether a split wait of an earlier launch gave up on `workspace`, for
+ * callers that launch without sync_after_launch.  No counterpart in the
+ * reference, whose launches never wait on each other's workgroups.
+ * `workspace` is a workspace given to shaobo_fa3_bwd_v2 / _on_stream /
+ * shaobo_fa3_bwd / shaobo_fa3_bwd_fused5 (NULL: the no-allocation scratch
+ * array of the current GPU).  Synchronises `stream` (a hipStream_t of the
+ * current GPU; NULL = the null stream), so queue it behind the launches to
+ * check, then reads the workspace's error word.  Returns
+ * SHAOBO_FA3_STATUS_HIP_ERROR when a launch of this process wrote it there
+ * (its gradients are wrong) and clears the word, so each give-up is
+ * reported once; SUCCESS otherwise, whatever an uninitialised workspace
+ * holds; INVALID_VALUE for a stream of another GPU. */
+int shaobo_fa3_ext_split_status(const void* workspace, void* stream);
+
+/* The number of split waits that gave up on the current GPU since the
+ * library was loaded, in any launch on any workspace: *count never
+ * decreases, so a caller that does not keep its workspaces (a framework
+ * binding allocating one per call) compares it with the count it saw last.
+ * No counterpart in the reference.  Synchronises `stream` first (as for
+ * shaobo_fa3_ext_split_status).  Returns SUCCESS, INVALID_VALUE (null
+ * count, or a stream of another GPU) or HIP_ERROR. */
+int shaobo_fa3_ext_split_error_count(void* stream, unsigned long long* count);
 
 /* shaobo_fa3_bwd_v2_on_stream that also records three caller-created
  * hipEvent_t on `stream`: events[0] before the delta preprocess, events[1]

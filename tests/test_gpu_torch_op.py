@@ -126,3 +126,31 @@ def test_autograd_attention():
             err = (got.float() - want).abs().max() / want.abs().max()
             assert err < 1e-2, float(err)
         q.grad = None
+
+
+def test_op_split_errors_reported_at_check():
+    """The op never synchronises, so a split wait that gives up cannot fail
+    the call; shaobo_fa3_torch.check_split_errors() -- the op's
+    synchronisation point -- raises for it once, and passes again after a
+    correct call."""
+    import shaobo_fa3_torch as T
+    log("[case] torch op: split give-up reported by check_split_errors")
+    lib = F.load()
+    g = O.golden(1, 2, 2, 1024, 128, True)  # split plan
+    args = inputs(g)
+    try:  # baseline: give-ups that earlier tests forced on purpose are consumed
+        T.check_split_errors()
+    except RuntimeError:
+        pass
+    lib.shaobo_fa3_ext_set_split_spin_limit(0)
+    try:
+        op(args, True, g["scale"])
+    finally:
+        lib.shaobo_fa3_ext_set_split_spin_limit(1 << 24)
+    with pytest.raises(RuntimeError, match="split wait"):
+        T.check_split_errors()
+    dq, dk, dv, delta = op(args, True, g["scale"])
+    T.check_split_errors()
+    res = {"dq": dq.float().cpu().numpy(), "dk": dk.float().cpu().numpy(),
+           "dv": dv.float().cpu().numpy(), "delta": delta.cpu().numpy()}
+    check(res, g)

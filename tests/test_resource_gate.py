@@ -31,8 +31,10 @@ def test_shipped_kernels_present(gated):
         assert any(want in n for n in names), want
     # every (head dim, causal, bf16) instantiation of the main kernel with
     # scaled and unscaled resident operands, and the split-plan
-    # instantiations of the causal ones (unscaled only)
-    assert sum("bwd_main_kernel" in n for n in names) == 20
+    # instantiations of the causal ones (unscaled only): 20, each with its
+    # race-check twin (shaobo_fa3_ext_set_race_check), which the gate holds
+    # to the same budget
+    assert sum("bwd_main_kernel" in n for n in names) == 40
 
 
 def test_main_kernel_two_waves_per_simd(gated):
