@@ -20,7 +20,13 @@ line: TFLOP/s from FLOPs = 10*B*H*S^2*D*0.5, ms per backward, % of fp16 dense
 MFMA peak, the main kernel's (MFMA) and the preprocess's (HBM) rooflines,
 and the CPU oracle timed on the host as the reported CPU baseline.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config P3]
+--all measures every BASELINE config (P1-P5) in one run and prints one JSON
+line per config (GPU ms per backward, TFLOP/s, % of peak, the main kernel's
+time, and the CPU oracle's backward of the whole config on the host, with
+the threads it used and the host's core count), then a markdown table of
+the same figures on stderr.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config P3] [--all]
 """
 import argparse
 import ctypes
@@ -122,6 +128,36 @@ def preprocess_bytes(B, Hq, S, D):
     return 2 * rows * D * 2 + rows * 4 * 4
 
 
+def host_cores():
+    """CPUs this process may run on (its affinity mask)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+# The oracle runs on at most this many threads: a GPU box gives one GPU a
+# 16-core share of its host, whatever the affinity mask shows.
+CPU_SHARE_PER_GPU = 16
+
+
+def cpu_full(cfg):
+    """The CPU oracle's fp32 backward of the whole config on the host's
+    cores (forward first, untimed): ms, threads, TFLOP/s."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import fa3_oracle as O
+    B, Hq, Hkv, S, D, causal = cfg
+    scale = 1.0 / math.sqrt(D)
+    threads = O.default_threads()
+    x = O.make_inputs(B, Hq, Hkv, S, D)
+    out, smax, ssum, _ = O.forward(x["q"], x["k"], x["v"], causal, scale, None, threads)
+    t0 = time.perf_counter()
+    O.backward(x["q"], x["k"], x["v"], out, x["dout"], smax, ssum, causal, scale, None, threads)
+    sec = time.perf_counter() - t0
+    return {"bwd_ms": round(sec * 1e3, 3), "threads": threads, "host_cores": host_cores(),
+            "tflops": round(flops(B, Hq, S, D, causal) / sec / 1e12, 6)}
+
+
 def cpu_baseline(cfg, budget_s):
     """Time the CPU oracle (fp32) on the host: its threaded backward on a
     bounded sample of the same workload -- whole (batch, kv-head) groups of
@@ -163,6 +199,9 @@ def cpu_baseline(cfg, budget_s):
         single[name] = {"bwd_ms": round(dt * 1e3, 3),
                         "tflops": round(flops(b1, hq1, s1, d1, c1) / dt / 1e12, 6)}
     return {"value": round(f / sec / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "host_cores": host_cores(),
+            "threads_note": f"threads = min(host cores, {CPU_SHARE_PER_GPU}): the GPU box's "
+                            "CPU share per GPU",
             "kind": "port",
             "sample": f"oracle fp32 backward of {sample_heads} of {B * Hq} query heads "
                       f"(S={S}, D={D}, causal={causal}), {runs} runs, {sec * 1e3:.1f} ms each",
@@ -171,38 +210,14 @@ def cpu_baseline(cfg, budget_s):
             "single_thread_bwd": single}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=None,
-                    help="untimed warm-up steps (default 20); warm-up also lasts at least "
-                         "0.3 s of GPU work, which brings the clocks to their steady state")
-    ap.add_argument("--config", default="P3", choices=sorted(CONFIGS))
-    ap.add_argument("--deterministic", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=10.0,
-                    help="seconds of CPU oracle work for cpu_baseline (0 disables)")
-    ap.add_argument("--calib-copy-mb", type=int, default=0,
-                    help="after timing, run a plain device copy of this many MiB "
-                         "(reference kernel for rocprofv3 byte counters)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path "
-              f"(--gpus {args.gpus} requested); the backward shards by (batch, kv-head) "
-              f"with no communication, so per-GPU throughput is the N=1 figure.",
-              file=sys.stderr)
-        sys.exit(2)
-
-    import torch
-    import shaobo_fa3 as F
-
-    B, Hq, Hkv, S, D, causal = CONFIGS[args.config]
+def measure(torch, lib, F, hip, name, steps, warmup, deterministic):
+    """GPU figures of one config: the timed backward calls, the per-kernel
+    durations back to back, and the rooflines (no CPU baseline)."""
+    B, Hq, Hkv, S, D, causal = CONFIGS[name]
     scale = 1.0 / math.sqrt(D)
-    lib = F.load()
-    hip = Hip()
     q, k, v, do, out, lse = make_inputs(torch, B, Hq, Hkv, S, D, causal, scale)
     p = F.make_params(lib, batch=B, seqlen=S, heads_q=Hq, heads_kv=Hkv, head_dim=D,
-                      causal=causal, softmax_scale=scale, deterministic=args.deterministic)
+                      causal=causal, softmax_scale=scale, deterministic=deterministic)
     nbytes = lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
     ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
@@ -216,32 +231,30 @@ def main():
         if st != F.SUCCESS:
             raise RuntimeError("shaobo_fa3_bwd_v2: " + F.status_name(st))
 
-    # Warm-up: at least `warmup` steps (default 20) and at least 0.3 s of
-    # GPU work, in batches of 20 -- the GPU's clocks ramp up over tens of
-    # milliseconds of sustained work, and a handful of steps measures the
-    # ramp instead of the kernel.
-    want = 20 if args.warmup is None else args.warmup
+    # Warm-up: at least `warmup` steps and at least 0.3 s of GPU work, in
+    # batches of 20 -- the GPU's clocks ramp up over tens of milliseconds of
+    # sustained work, and a handful of steps measures the ramp instead of
+    # the kernel.
     done = 0
     t_w = time.perf_counter()
-    while done < want or time.perf_counter() - t_w < 0.3:
+    while done < warmup or time.perf_counter() - t_w < 0.3:
         for _ in range(20):
             step()
         done += 20
         torch.cuda.synchronize()
     warm_s = time.perf_counter() - t_w
-    args.warmup = want
 
     # ---- timed region: exactly `steps` backward lifecycles ----
     e0, e1 = hip.event(), hip.event()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     hip.record(e0)
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     hip.record(e1)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = hip.elapsed_ms(e0, e1) / args.steps
+    ms = hip.elapsed_ms(e0, e1) / steps
     f = flops(B, Hq, S, D, causal)
     tflops = f / (ms * 1e-3) / 1e12
 
@@ -257,11 +270,11 @@ def main():
         main_step()
     torch.cuda.synchronize()
     hip.record(e0)
-    for _ in range(args.steps):
+    for _ in range(steps):
         main_step()
     hip.record(e1)
     torch.cuda.synchronize()
-    main_ms = hip.elapsed_ms(e0, e1) / args.steps
+    main_ms = hip.elapsed_ms(e0, e1) / steps
     pre_step_ms = ms - main_ms
     # the preprocess alone: the dot_do_o component runs the same kernel on
     # the same rows (delta plus the packed sidecar: the same bytes)
@@ -280,49 +293,49 @@ def main():
         pre_step()
     torch.cuda.synchronize()
     hip.record(e0)
-    for _ in range(args.steps):
+    for _ in range(steps):
         pre_step()
     hip.record(e1)
     torch.cuda.synchronize()
-    pre_alone_ms = hip.elapsed_ms(e0, e1) / args.steps
+    pre_alone_ms = hip.elapsed_ms(e0, e1) / steps
     # the same number of calls through the timed entry, three events per
     # call, read after one sync (marker-inclusive durations)
-    evs = [[hip.event() for _ in range(3)] for _ in range(args.steps)]
+    evs = [[hip.event() for _ in range(3)] for _ in range(steps)]
     ev_arrays = [(ctypes.c_void_p * 3)(*[e.value for e in trio]) for trio in evs]
-    for i in range(args.steps):
+    for i in range(steps):
         st = lib.shaobo_fa3_ext_bwd_v2_timed(*argv, ctypes.byref(p), None, ev_arrays[i])
         if st != F.SUCCESS:
             raise RuntimeError("shaobo_fa3_ext_bwd_v2_timed: " + F.status_name(st))
     torch.cuda.synchronize()
-    pre_marked = sum(hip.elapsed_ms(t[0], t[1]) for t in evs) / args.steps
-    main_marked = sum(hip.elapsed_ms(t[1], t[2]) for t in evs) / args.steps
-    staged_ms = hip.elapsed_ms(evs[0][0], evs[-1][2]) / args.steps
+    pre_marked = sum(hip.elapsed_ms(t[0], t[1]) for t in evs) / steps
+    main_marked = sum(hip.elapsed_ms(t[1], t[2]) for t in evs) / steps
+    staged_ms = hip.elapsed_ms(evs[0][0], evs[-1][2]) / steps
     main_tflops = f / (main_ms * 1e-3) / 1e12
     pre_gbs = preprocess_bytes(B, Hq, S, D) / (pre_step_ms * 1e-3) / 1e9
-    traffic = load_traffic(args.config)
-    result = {
+    return {
         "metric": METRIC,
         "value": round(tflops, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic",
-        "config": {"workload": f"fa3_bwd_v2 {args.config} B{B} Hq{Hq} Hkv{Hkv} S{S} D{D} "
+        "config": {"workload": f"fa3_bwd_v2 {name} B{B} Hq{Hq} Hkv{Hkv} S{S} D{D} "
                                f"{'causal' if causal else 'full'}",
                    "batch": B, "heads_q": Hq, "heads_kv": Hkv, "seq_len": S, "head_dim": D,
-                   "causal": causal, "deterministic": args.deterministic,
+                   "causal": causal, "deterministic": deterministic,
                    "flops_per_bwd": f},
         "pct_fp16_peak": round(100.0 * tflops / FP16_PEAK_TFLOPS, 3),
         "wall_s_timed": round(wall, 4),
         "warmup_steps_run": done,
         "warmup_s": round(warm_s, 3),
-        "kernels_ms": {"preprocess_kernel": round(pre_step_ms, 5), "bwd_main_kernel": round(main_ms, 5),
+        "kernels_ms": {"preprocess_kernel": round(pre_step_ms, 5),
+                       "bwd_main_kernel": round(main_ms, 5),
                        "preprocess_alone_back_to_back": round(pre_alone_ms, 5)},
         "kernels_ms_marked": {"preprocess_kernel": round(pre_marked, 5),
                               "bwd_main_kernel": round(main_marked, 5),
@@ -331,12 +344,81 @@ def main():
                      "achieved": round(main_tflops, 3),
                      "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(main_tflops / FP16_PEAK_TFLOPS, 5),
-                     "traffic": traffic},
+                     "traffic": load_traffic(name),
+                     "traffic_source": "profiles/traffic_bwd_main_kernel.json (rocprofv3 "
+                                       "FETCH_SIZE + WRITE_SIZE of this kernel, calibrated)"},
         "preprocess_roofline": {"kernel": "preprocess_kernel", "bound": "hbm",
                                 "achieved": round(pre_gbs, 1), "peak": HBM_PEAK_GBS,
                                 "unit": "GB/s", "frac": round(pre_gbs / HBM_PEAK_GBS, 5),
                                 "bytes": preprocess_bytes(B, Hq, S, D)},
     }
+
+
+def run_all(torch, lib, F, hip, args):
+    """Every BASELINE config: one JSON line each (GPU figures, the whole
+    config's CPU oracle backward), then a markdown table on stderr."""
+    rows = []
+    for name in ("P1", "P2", "P3", "P4", "P5"):
+        B, Hq, Hkv, S, D, causal = CONFIGS[name]
+        # about 0.5 s of timed GPU work per config (at ~40 % of peak), 10..200 calls
+        est_ms = flops(B, Hq, S, D, causal) / (0.4 * FP16_PEAK_TFLOPS * 1e12) * 1e3 + 0.02
+        steps = max(10, min(200, int(500 / est_ms)))
+        r = measure(torch, lib, F, hip, name, steps, 20, args.deterministic)
+        torch.cuda.empty_cache()
+        line = {"config": name, "workload": r["config"]["workload"],
+                "gpu_ms_per_bwd": r["ms_per_step"], "tflops": r["value"],
+                "pct_fp16_peak": r["pct_fp16_peak"], "steps": steps,
+                "main_kernel_ms": r["kernels_ms"]["bwd_main_kernel"],
+                "preprocess_ms": r["kernels_ms"]["preprocess_kernel"],
+                "main_kernel_frac": r["roofline"]["frac"]}
+        if args.cpu_budget > 0:
+            line["cpu"] = cpu_full(CONFIGS[name])
+        print(json.dumps(line), flush=True)
+        rows.append(line)
+    out = ["| Config | CPU bwd ms (threads / host cores) | GPU ms/bwd | GPU TFLOP/s | "
+           "% fp16 peak | main kernel ms |", "|---|---|---|---|---|---|"]
+    for r in rows:
+        cpu = r.get("cpu")
+        cpu_s = f"{cpu['bwd_ms']:.1f} ({cpu['threads']} / {cpu['host_cores']})" if cpu else "-"
+        out.append(f"| {r['workload']} | {cpu_s} | {r['gpu_ms_per_bwd']:.5f} | {r['tflops']:.1f} "
+                   f"| {r['pct_fp16_peak']:.2f} | {r['main_kernel_ms']:.5f} |")
+    print("\n".join(out), file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warm-up steps (default 20); warm-up also lasts at least "
+                         "0.3 s of GPU work, which brings the clocks to their steady state")
+    ap.add_argument("--config", default="P3", choices=sorted(CONFIGS))
+    ap.add_argument("--all", action="store_true",
+                    help="every config P1-P5, one JSON line each (GPU and whole-config CPU)")
+    ap.add_argument("--deterministic", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0,
+                    help="seconds of CPU oracle work for cpu_baseline (0 disables)")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="after timing, run a plain device copy of this many MiB "
+                         "(reference kernel for rocprofv3 byte counters)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested); the backward shards by (batch, kv-head) "
+              f"with no communication, so per-GPU throughput is the N=1 figure.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import shaobo_fa3 as F
+
+    lib = F.load()
+    hip = Hip()
+    if args.all:
+        run_all(torch, lib, F, hip, args)
+        return
+    warmup = 20 if args.warmup is None else args.warmup
+    result = measure(torch, lib, F, hip, args.config, args.steps, warmup, args.deterministic)
     if args.calib_copy_mb > 0:
         # plain copy kernel of known size, for scaling rocprofv3 FETCH/WRITE_SIZE
         n = args.calib_copy_mb * (1 << 20) // 4
