@@ -34,7 +34,7 @@ void set_job_map(FusedArgs& a) {
 // 0.65 at kernel entry and between two units.  For each x the pair of
 // workgroups sharing a job is balanced: the head length minimises the later
 // of the two finishing times.
-void split_heads(int M, uint16_t* head_kv, uint16_t* head_q) {
+void split_heads(int M, int* head_kv, int* head_q) {
     constexpr double kQ = 0.73, kPro = 2.5, kEntry = 0.65, kGap = 0.65;
     constexpr double kWholeKv = 2.0, kWholeQ = 0.8;
     constexpr double kPubKv = 2.6, kAddKv = 2.8, kPubQ = 1.6, kAddQ = 1.8;
@@ -60,7 +60,7 @@ void split_heads(int M, uint16_t* head_kv, uint16_t* head_q) {
                 best = L;
             }
         }
-        head_kv[x] = (uint16_t)best;
+        head_kv[x] = best;
         // dQ query tile M + x (M + x + 1 tiles): head piece alone, remainder
         // after the whole dKV job of key tile M + x (M - x tiles)
         best = M + x + 1;
@@ -76,7 +76,7 @@ void split_heads(int M, uint16_t* head_kv, uint16_t* head_q) {
                 best = L;
             }
         }
-        head_q[x] = (uint16_t)best;
+        head_q[x] = best;
     }
 }
 
@@ -334,7 +334,18 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
         a.part_q = reinterpret_cast<float*>(ws + plan.pq_off);
         a.part_kv_bytes = (uint32_t)(plan.pq_off - plan.pkv_off);
         a.part_q_bytes = (uint32_t)(plan.total - plan.pq_off);
-        split_heads(plan.bal_m, a.head_kv, a.head_q);
+        // each workgroup's descriptor: its job id's kind x = pos mod M (pos
+        // as the job map deals it), group and head-piece length
+        int head_kv[kMaxBalM], head_q[kMaxBalM];
+        split_heads(plan.bal_m, head_kv, head_q);
+        const int M = plan.bal_m;
+        if (a.n_jobs > kMaxSplitWgs) return hipErrorInvalidValue;  // plan_workspace: <= 512
+        for (int id = 0; id < a.n_jobs; ++id) {
+            int g = 0, pos = 0;
+            job_of(a, id, g, pos);
+            const int kind = pos / M, x = pos % M;
+            a.split_desc[id] = split_desc(kind, x, g, kind == 1 || kind == 2 ? head_kv[x] : head_q[x]);
+        }
     }
     if (g_debug_kernels.load()) launch_race_check(a, p.head_dim, p.causal, p.bf16, t.stream);
     else if (p.head_dim == 128) launch_dd<128, false>(a, p.causal, p.bf16, t.stream);

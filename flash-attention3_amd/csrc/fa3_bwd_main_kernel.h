@@ -67,6 +67,15 @@
 namespace fa3 {
 
 constexpr int kMaxBalM = 128;  // split plan: at most 512 jobs, so M = QT / 2 <= 128
+constexpr int kMaxSplitWgs = 4 * kMaxBalM;  // its workgroups: one per job
+
+// Split-plan workgroup descriptor (one 32-bit word per workgroup, built on
+// the host): bits 0..1 the workgroup's kind (see bwd_main_kernel), 2..9 x,
+// 10..19 the (batch, head) group, 20..29 the head-piece length of the split
+// job it works on (tiles; a length covering the whole job leaves it unsplit).
+__host__ __device__ constexpr uint32_t split_desc(int kind, int x, int g, int len) {
+    return (uint32_t)kind | ((uint32_t)x << 2) | ((uint32_t)g << 10) | ((uint32_t)len << 20);
+}
 
 struct FusedArgs {
     const _Float16* q;
@@ -121,11 +130,10 @@ struct FusedArgs {
     // bwd_main_kernel.  Synchronisation words and partial sums live in the
     // workspace.
     int bal_m;
-    // head-piece lengths (tiles) of the long jobs, x in [0, bal_m): dKV job of
-    // key tile x and dQ job of query tile bal_m + x; a length that covers the
-    // whole job means that job is not split
-    uint16_t head_kv[kMaxBalM];
-    uint16_t head_q[kMaxBalM];
+    // one descriptor per workgroup (split_desc): a workgroup reads its own
+    // word and the arguments its units' set-up needs in one batch of scalar
+    // loads, so its first tile loads go out after one argument round trip
+    uint32_t split_desc[kMaxSplitWgs];
     // Split-job synchronisation (see split_arrive / split_end): per split job
     // an arrival word and a ready word, compared with this launch's epoch, so
     // nothing needs clearing between launches.  dKV jobs first, then dQ jobs.
@@ -1449,7 +1457,7 @@ __device__ __forceinline__ void unit_gap() {
 
 // Job id -> (group, position in the group); see the job map below.
 template <typename A>
-__device__ __forceinline__ void job_of(const A& a, int id, int& g, int& pos) {
+__host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int& pos) {
     if (a.xcd_parts > 0) {
         const int xcd = id & 7;
         const int n = id >> 3;
@@ -1507,14 +1515,24 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     const int QT = a.seqlen / 64;
     int g, pos;
     if constexpr (kSplit) {
-        job_of(a, blockIdx.x, g, pos);
+        // the workgroup's descriptor and every argument the units' set-up
+        // reads before its first loads, requested together: without the asm
+        // the compiler issues them branch by branch, one dependent round
+        // trip each (P3: ~1.6 us from entry to the first load)
+        const uint32_t desc = a.split_desc[blockIdx.x];
+        __asm__ volatile("" ::"s"(desc), "s"(a.div_hkv.mul), "s"(a.div_hkv.shr), "s"(a.heads_kv),
+                         "s"(a.heads_q), "s"(a.group), "s"(a.bal_m), "s"(a.seqlen), "s"(a.q_rs),
+                         "s"(a.q_hs), "s"(a.kv_rs), "s"(a.kv_hs), "s"(a.q), "s"(a.k), "s"(a.v),
+                         "s"(a.dout), "s"(a.nlse2), "s"(a.ndelta));
+        const int kind = desc & 3, x = (desc >> 2) & 255, len = desc >> 20;
+        g = (desc >> 10) & 1023;
         // G = 1: group g is query head g (and KV head g) of batch b
         const int b = fdiv(a.div_hkv, g), h = g - b * a.heads_kv;
         const int M = a.bal_m;
         const int job0 = g * M;
-        if (pos < M) {
+        if (kind == 0) {
             // dKV key tile M + x whole, then the remainder of dQ query tile M + x
-            const int x = pos, nq = M + x + 1, lq = a.head_q[x];
+            const int nq = M + x + 1, lq = len;
             debug_poison<D, kDebug>(smem);
             dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, M + x, M + x, QT, -1,
                                                                 smem);
@@ -1524,9 +1542,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
                 dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, M + x, lq, nq,
                                                                    2 * (job0 + x) + 1, smem);
             }
-        } else if (pos < 2 * M) {
+        } else if (kind == 1) {
             // dQ query tile x whole, then the remainder of dKV key tile x
-            const int x = pos - M, nkv = QT - x, lkv = a.head_kv[x];
+            const int nkv = QT - x, lkv = len;
             debug_poison<D, kDebug>(smem);
             dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, x, 0, x + 1, -1,
                                                                smem);
@@ -1536,15 +1554,15 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
                 dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, x, x + lkv, QT,
                                                                     2 * (job0 + x) + 1, smem);
             }
-        } else if (pos < 3 * M) {
+        } else if (kind == 2) {
             // head piece (or all) of dKV key tile x
-            const int x = pos - 2 * M, nkv = QT - x, lkv = a.head_kv[x];
+            const int nkv = QT - x, lkv = len;
             debug_poison<D, kDebug>(smem);
             dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(
                 a, a, b, h, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1, smem);
         } else {
             // head piece (or all) of dQ query tile M + x
-            const int x = pos - 3 * M, nq = M + x + 1, lq = a.head_q[x];
+            const int nq = M + x + 1, lq = len;
             debug_poison<D, kDebug>(smem);
             dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(
                 a, a, b, h, h, M + x, 0, min(lq, nq), lq < nq ? 2 * (job0 + x) : -1, smem);
