@@ -2,11 +2,15 @@
 // side (job map, split plan, workspace plan, launch).  The kernels and their
 // device helpers are in fa3_bwd_main_kernel.h.
 #include "fa3_bwd_main_kernel.h"
+#include "fa3_split_plan.h"
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <memory>
 #include <mutex>
 #include <random>
+#include <vector>
 
 namespace fa3 {
 namespace {
@@ -23,61 +27,6 @@ void set_job_map(FusedArgs& a) {
     a.div_parts = make_fastdiv(a.xcd_parts);
     a.div_part_len = make_fastdiv(a.part_len);
     a.div_jpg = make_fastdiv(a.jobs_per_group);
-}
-
-// Head-piece lengths of the split plan.  Workgroup times in units of one dKV
-// step, measured on MI355X at B1 H4 S2048 D128 (per-workgroup timestamps):
-// a dQ step costs 0.73, a unit's prologue (loads + first score phase) 2.5,
-// its epilogue 2.0 (dKV) / 0.8 (dQ) for a whole job; of a split job, the
-// piece that arrives first spends kPub (storing its partial sums) and the
-// second, after waiting for them, kAdd (adding them and writing the output);
-// 0.65 at kernel entry and between two units.  For each x the pair of
-// workgroups sharing a job is balanced: the head length minimises the later
-// of the two finishing times.
-void split_heads(int M, int* head_kv, int* head_q) {
-    constexpr double kQ = 0.73, kPro = 2.5, kEntry = 0.65, kGap = 0.65;
-    constexpr double kWholeKv = 2.0, kWholeQ = 0.8;
-    constexpr double kPubKv = 2.6, kAddKv = 2.8, kPubQ = 1.6, kAddQ = 1.8;
-    // a, b: the two workgroups' times up to the end of their last steps
-    auto pair_end = [](double a, double b, double pub, double add) {
-        const double first = a < b ? a : b, second = a < b ? b : a;
-        return (second > first + pub ? second : first + pub) + add;
-    };
-    const int QT = 2 * M;
-    for (int x = 0; x < M; ++x) {
-        // dKV key tile x (QT - x tiles): head piece alone, remainder after
-        // the whole dQ job of query tile x
-        int best = QT - x;
-        double best_t = 1e30;
-        for (int L = 1; L <= QT - x; ++L) {
-            const int r = QT - x - L;
-            const double c = kEntry + kPro + (L - 1);
-            const double b = kEntry + kPro + x * kQ + kWholeQ;
-            const double t = r > 0 ? pair_end(c, b + kGap + kPro + (r - 1), kPubKv, kAddKv)
-                                   : (c + kWholeKv > b ? c + kWholeKv : b);
-            if (t < best_t) {
-                best_t = t;
-                best = L;
-            }
-        }
-        head_kv[x] = best;
-        // dQ query tile M + x (M + x + 1 tiles): head piece alone, remainder
-        // after the whole dKV job of key tile M + x (M - x tiles)
-        best = M + x + 1;
-        best_t = 1e30;
-        for (int L = 1; L <= M + x + 1; ++L) {
-            const int r = M + x + 1 - L;
-            const double d = kEntry + kPro + (L - 1) * kQ;
-            const double av = kEntry + kPro + (M - x - 1) + kWholeKv;
-            const double t = r > 0 ? pair_end(d, av + kGap + kPro + (r - 1) * kQ, kPubQ, kAddQ)
-                                   : (d + kWholeQ > av ? d + kWholeQ : av);
-            if (t < best_t) {
-                best_t = t;
-                best = L;
-            }
-        }
-        head_q[x] = best;
-    }
 }
 
 FusedArgs base_args(const BwdProblem& p, const BwdTensors& t) {
@@ -335,16 +284,17 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
         a.part_kv_bytes = (uint32_t)(plan.pq_off - plan.pkv_off);
         a.part_q_bytes = (uint32_t)(plan.total - plan.pq_off);
         // each workgroup's descriptor: its job id's kind x = pos mod M (pos
-        // as the job map deals it), group and head-piece length
-        int head_kv[kMaxBalM], head_q[kMaxBalM];
-        split_heads(plan.bal_m, head_kv, head_q);
+        // as the job map deals it), group, head-piece length and short job
         const int M = plan.bal_m;
-        if (a.n_jobs > kMaxSplitWgs) return hipErrorInvalidValue;  // plan_workspace: <= 512
+        if (a.n_jobs > kMaxSplitWgs || a.n_groups > 64) return hipErrorInvalidValue;
+        const SplitPlan& sp = split_plan(M);
         for (int id = 0; id < a.n_jobs; ++id) {
             int g = 0, pos = 0;
             job_of(a, id, g, pos);
             const int kind = pos / M, x = pos % M;
-            a.split_desc[id] = split_desc(kind, x, g, kind == 1 || kind == 2 ? head_kv[x] : head_q[x]);
+            const int len = kind == 1 || kind == 2 ? sp.head_kv[x] : sp.head_q[x];
+            const int s = kind == 1 ? sp.short_kv[x] : kind == 3 ? sp.short_q[x] : -1;
+            a.split_desc[id] = split_desc(kind, x, g, len, s < 0 ? kNoShort : s);
         }
     }
     if (g_debug_kernels.load()) launch_race_check(a, p.head_dim, p.causal, p.bf16, t.stream);

@@ -63,18 +63,23 @@
 
 #include "fa3_bwd_device.h"
 #include "fa3_bwd_internal.h"
+#include "fa3_split_plan.h"
 
 namespace fa3 {
 
-constexpr int kMaxBalM = 128;  // split plan: at most 512 jobs, so M = QT / 2 <= 128
 constexpr int kMaxSplitWgs = 4 * kMaxBalM;  // its workgroups: one per job
 
 // Split-plan workgroup descriptor (one 32-bit word per workgroup, built on
-// the host): bits 0..1 the workgroup's kind (see bwd_main_kernel), 2..9 x,
-// 10..19 the (batch, head) group, 20..29 the head-piece length of the split
-// job it works on (tiles; a length covering the whole job leaves it unsplit).
-__host__ __device__ constexpr uint32_t split_desc(int kind, int x, int g, int len) {
-    return (uint32_t)kind | ((uint32_t)x << 2) | ((uint32_t)g << 10) | ((uint32_t)len << 20);
+// the host): bits 0..1 the workgroup's kind (see bwd_main_kernel), 2..8 x,
+// 9..14 the (batch, head) group, 15..23 the head-piece length of the split
+// job it works on (tiles; a length covering the whole job leaves it
+// unsplit), 24..31 the short dQ job (query tile < M) that a kind 1 or 3
+// workgroup runs first, or kNoShort.  The split plan has at most 512 jobs
+// and S / 64 >= 4, so M <= 128, groups <= 64 and lengths <= 256 fit.
+constexpr int kNoShort = 255;
+__host__ __device__ constexpr uint32_t split_desc(int kind, int x, int g, int len, int shrt) {
+    return (uint32_t)kind | ((uint32_t)x << 2) | ((uint32_t)g << 9) | ((uint32_t)len << 15) |
+           ((uint32_t)shrt << 24);
 }
 
 struct FusedArgs {
@@ -1485,18 +1490,19 @@ __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int&
 // Split plan (bal_m = M = QT / 2 > 0; causal, G = 1, few jobs): the causal
 // jobs run 1 .. QT steps, so one long job would set the kernel's length.
 // The long jobs (dKV key tiles x < M, dQ query tiles M + x) are cut into a
-// head piece of head_kv[x] / head_q[x] tiles and a remainder, and each
-// remainder shares a workgroup with a short job of the other role
-// (x = p mod M):
-//   p in [0, M):    dKV key tile M + x (whole), then the remainder of dQ
-//                   query tile M + x (key tiles head_q[x] .. M + x);
-//   p in [M, 2M):   dQ query tile x (whole), then the remainder of dKV key
-//                   tile x (query tiles x + head_kv[x] .. QT - 1);
-//   p in [2M, 3M):  head piece of dKV key tile x;
-//   p in [3M, 4M):  head piece of dQ query tile M + x.
-// The host picks the head lengths from a cost model of the steps, prologues
-// and epilogues so that the workgroups finish together (a length covering
-// the whole job leaves it unsplit).
+// head piece and a remainder, and the short jobs are spread over the
+// workgroups that have time for them.  Each workgroup has a descriptor
+// (split_desc) with its kind, x, group, head length and short job:
+//   kind 0:  dKV key tile M + x (whole), then the remainder of dQ query tile
+//            M + x (key tiles len .. M + x);
+//   kind 1:  the short dQ job (query tile < M, whole) if any, then the
+//            remainder of dKV key tile x (query tiles x + len .. QT - 1);
+//   kind 2:  head piece of dKV key tile x (len tiles);
+//   kind 3:  the short dQ job if any, then the head piece of dQ query tile
+//            M + x (len tiles).
+// The host picks the head lengths and the short jobs' places from a cost
+// model of the steps, prologues and epilogues, so that the workgroups
+// finish together (a length covering the whole job leaves it unsplit).
 //
 // kSplit selects the split plan (a separate instantiation: its units issue
 // their loads at a different point of the step, see dkv_role's score).
@@ -1524,8 +1530,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
                          "s"(a.heads_q), "s"(a.group), "s"(a.bal_m), "s"(a.seqlen), "s"(a.q_rs),
                          "s"(a.q_hs), "s"(a.kv_rs), "s"(a.kv_hs), "s"(a.q), "s"(a.k), "s"(a.v),
                          "s"(a.dout), "s"(a.nlse2), "s"(a.ndelta));
-        const int kind = desc & 3, x = (desc >> 2) & 255, len = desc >> 20;
-        g = (desc >> 10) & 1023;
+        const int kind = desc & 3, x = (desc >> 2) & 127, len = (desc >> 15) & 511;
+        const int shrt = desc >> 24;
+        g = (desc >> 9) & 63;
         // G = 1: group g is query head g (and KV head g) of batch b
         const int b = fdiv(a.div_hkv, g), h = g - b * a.heads_kv;
         const int M = a.bal_m;
@@ -1543,13 +1550,16 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
                                                                    2 * (job0 + x) + 1, smem);
             }
         } else if (kind == 1) {
-            // dQ query tile x whole, then the remainder of dKV key tile x
+            // the short dQ job (query tile shrt, whole) if any, then the
+            // remainder of dKV key tile x
             const int nkv = QT - x, lkv = len;
-            debug_poison<D, kDebug>(smem);
-            dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, x, 0, x + 1, -1,
-                                                               smem);
+            if (shrt != kNoShort) {
+                debug_poison<D, kDebug>(smem);
+                dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
+                                                                   shrt + 1, -1, smem);
+                if (lkv < nkv) unit_gap<2 * (D / 64)>();
+            }
             if (lkv < nkv) {
-                unit_gap<2 * (D / 64)>();
                 debug_poison<D, kDebug>(smem);
                 dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, x, x + lkv, QT,
                                                                     2 * (job0 + x) + 1, smem);
@@ -1561,8 +1571,15 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
             dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(
                 a, a, b, h, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1, smem);
         } else {
+            // the short dQ job (query tile shrt, whole) if any, then the
             // head piece (or all) of dQ query tile M + x
             const int nq = M + x + 1, lq = len;
+            if (shrt != kNoShort) {
+                debug_poison<D, kDebug>(smem);
+                dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
+                                                                   shrt + 1, -1, smem);
+                unit_gap<2 * (D / 64)>();
+            }
             debug_poison<D, kDebug>(smem);
             dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(
                 a, a, b, h, h, M + x, 0, min(lq, nq), lq < nq ? 2 * (job0 + x) : -1, smem);

@@ -1,0 +1,46 @@
+// CPU check of the split plan's planner (flash-attention3_amd/csrc/fa3_split_plan.h),
+// built under ASan + UBSan: for every M the kernel can receive (2 .. 128),
+//   * each short dQ job (query tiles 0 .. M - 1) is placed exactly once, on a
+//     dKV pair's remainder workgroup or a dQ pair's head-piece workgroup;
+//   * every head length lies in 1 .. the job's tile count (the kernel's
+//     descriptor holds it in 9 bits);
+//   * the planner's modelled finishing time is no later than that of the
+//     fixed pairing it replaces (dKV pair x runs short job x, dQ pairs none),
+//     each pair at its best head length under the same model.
+// Exit status 0 when all hold.
+#include <cstdio>
+#include <vector>
+
+#include "fa3_split_plan.h"
+
+int main() {
+    using namespace fa3;
+    int bad = 0;
+    for (int M = 2; M <= kMaxBalM; ++M) {
+        const SplitPlan& p = split_plan(M);
+        const int QT = 2 * M;
+        std::vector<int> seen(M, 0);
+        double planned = 0, fixed = 0;
+        int h = 0;
+        for (int x = 0; x < M; ++x) {
+            for (int s : {p.short_kv[x], p.short_q[x]}) {
+                if (s >= M || s < -1) ++bad;
+                else if (s >= 0) ++seen[s];
+            }
+            if (p.head_kv[x] < 1 || p.head_kv[x] > QT - x || p.head_kv[x] > 511) ++bad;
+            if (p.head_q[x] < 1 || p.head_q[x] > M + x + 1 || p.head_q[x] > 511) ++bad;
+            planned = std::max(planned, plan_model::kv_pair(QT, x, p.short_kv[x], &h));
+            planned = std::max(planned, plan_model::q_pair(M, x, p.short_q[x], &h));
+            fixed = std::max(fixed, plan_model::kv_pair(QT, x, x, &h));
+            fixed = std::max(fixed, plan_model::q_pair(M, x, -1, &h));
+        }
+        for (int s = 0; s < M; ++s)
+            if (seen[s] != 1) ++bad;
+        if (planned > fixed + 1e-9) ++bad;
+        if (M == 16 || bad)
+            std::printf("M=%d modelled %.2f (fixed pairing %.2f) problems so far %d\n", M, planned,
+                        fixed, bad);
+    }
+    std::printf("%s\n", bad ? "FAIL" : "ok");
+    return bad ? 1 : 0;
+}

@@ -3,7 +3,9 @@ and UndefinedBehaviorSanitizer while a fuzzer drives every validation,
 workspace query and entry point with random parameter structs
 (tests/sanitize/abi_fuzz.cpp), and the CPU oracle under ASan + UBSan and
 under ThreadSanitizer (tests/sanitize/oracle_run.cpp), and the kernels'
-host-computed fast division against / under UBSan (tests/sanitize/fastdiv_check.cpp).  Built by
+host-computed fast division against / under UBSan (tests/sanitize/fastdiv_check.cpp),
+and the split plan's planner against its invariants under ASan + UBSan
+(tests/sanitize/split_plan_check.cpp).  Built by
 tests/sanitize/Makefile."""
 import os
 import shutil
@@ -28,7 +30,8 @@ def built():
 
 
 @pytest.mark.parametrize("exe,args", [("abi_asan", ["20000"]), ("oracle_asan", []),
-                                      ("oracle_tsan", []), ("fastdiv_ubsan", [])])
+                                      ("oracle_tsan", []), ("fastdiv_ubsan", []),
+                                      ("split_plan_asan", [])])
 def test_sanitized_run_is_clean(built, exe, args):
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1",
                UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1",
