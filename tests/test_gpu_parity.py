@@ -310,8 +310,16 @@ def test_full_size_configs(B, Hq, Hkv, S, D, causal):
     g = O.golden(B, Hq, Hkv, S, D, causal)
     res = run_v2(g, torch)
     assert res["status"] == F.SUCCESS
+    check_per_group(res, g)
+
+
+def check_per_group(res, g):
+    """The bar on the whole tensors and on every (batch, kv-head) group: dK /
+    dV of the group's KV head, dQ / delta of its query heads."""
     rep = check(res, g)
     log({k: round(v["max_rel"], 6) for k, v in rep.items()})
+    B, Hq, _, _ = g["q"].shape
+    Hkv = g["k"].shape[1]
     G = Hq // Hkv
     worst = {}
     for b in range(B):
@@ -321,6 +329,27 @@ def test_full_size_configs(B, Hq, Hkv, S, D, causal):
             for n, m in check(res, g, sel=sel).items():
                 worst[n] = max(worst.get(n, 0.0), m["max_rel"])
     log({"worst group": {k: round(v, 6) for k, v in worst.items()}})
+
+
+@pytest.mark.parametrize("dtype,layout,scale", [
+    ("bf16", "bhsd", None),   # bf16 instantiation of the persistent plan
+    ("fp16", "bshd", None),   # BSHD strides in the persistent job loop
+    ("fp16", "bhsd", 1.0),    # scale 1: c = log2(e) > 1, the unscaled instantiation
+])
+def test_persistent_plan_variants(dtype, layout, scale):
+    """The persistent default plan (at least two jobs per CU: 640 jobs at B1
+    Hq8 Hkv2 S4096 D128 causal) in the instantiations the BASELINE configs do
+    not reach -- bf16, BSHD, unscaled resident operands -- against the
+    oracle, per (batch, kv-head) group; BSHD also bit-equal to BHSD."""
+    log(f"[case] persistent plan {dtype} {layout} scale={scale} B1 Hq8 Hkv2 S4096 D128 causal")
+    g = O.golden(1, 8, 2, 4096, 128, True, scale=scale, dtype=dtype)
+    res = run_v2(g, torch, bshd=layout == "bshd")
+    assert res["status"] == F.SUCCESS, F.status_name(res["status"])
+    check_per_group(res, g)
+    if layout == "bshd":
+        ref = run_v2(g, torch)
+        for n in ("dq", "dk", "dv", "delta"):
+            np.testing.assert_array_equal(res[n], ref[n])
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,S,D,causal", [
