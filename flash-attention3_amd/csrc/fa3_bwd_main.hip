@@ -293,7 +293,7 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
             job_of(a, id, g, pos);
             const int kind = pos / M, x = pos % M;
             const int len = kind == 1 || kind == 2 ? sp.head_kv[x] : sp.head_q[x];
-            const int s = kind == 1 ? sp.short_kv[x] : kind == 3 ? sp.short_q[x] : -1;
+            const int s = sp.shrt[kind][x];
             a.split_desc[id] = split_desc(kind, x, g, len, s < 0 ? kNoShort : s);
         }
     }

@@ -1492,14 +1492,16 @@ __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int&
 // The long jobs (dKV key tiles x < M, dQ query tiles M + x) are cut into a
 // head piece and a remainder, and the short jobs are spread over the
 // workgroups that have time for them.  Each workgroup has a descriptor
-// (split_desc) with its kind, x, group, head length and short job:
-//   kind 0:  dKV key tile M + x (whole), then the remainder of dQ query tile
-//            M + x (key tiles len .. M + x);
-//   kind 1:  the short dQ job (query tile < M, whole) if any, then the
-//            remainder of dKV key tile x (query tiles x + len .. QT - 1);
-//   kind 2:  head piece of dKV key tile x (len tiles);
-//   kind 3:  the short dQ job if any, then the head piece of dQ query tile
-//            M + x (len tiles).
+// (split_desc) with its kind, x, group, head length and short job (a
+// whole dQ job of query tile < M, if the plan places one there):
+//   kind 0:  dKV key tile M + x (whole), the short job, then the remainder
+//            of dQ query tile M + x (key tiles len .. M + x);
+//   kind 1:  the short job, then the remainder of dKV key tile x (query
+//            tiles x + len .. QT - 1);
+//   kind 2:  the short job, then the head piece of dKV key tile x (len
+//            tiles);
+//   kind 3:  the short job, then the head piece of dQ query tile M + x
+//            (len tiles).
 // The host picks the head lengths and the short jobs' places from a cost
 // model of the steps, prologues and epilogues, so that the workgroups
 // finish together (a length covering the whole job leaves it unsplit).
@@ -1538,13 +1540,21 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
         const int M = a.bal_m;
         const int job0 = g * M;
         if (kind == 0) {
-            // dKV key tile M + x whole, then the remainder of dQ query tile M + x
+            // dKV key tile M + x whole, the short dQ job (query tile shrt,
+            // whole) if any, then the remainder of dQ query tile M + x
             const int nq = M + x + 1, lq = len;
             debug_poison<D, kDebug>(smem);
             dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, M + x, M + x, QT, -1,
                                                                 smem);
-            if (lq < nq) {
+            if (shrt != kNoShort) {
                 unit_gap<4 * (D / 64)>();
+                debug_poison<D, kDebug>(smem);
+                dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
+                                                                   shrt + 1, -1, smem);
+            }
+            if (lq < nq) {
+                if (shrt != kNoShort) unit_gap<2 * (D / 64)>();
+                else unit_gap<4 * (D / 64)>();
                 debug_poison<D, kDebug>(smem);
                 dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, M + x, lq, nq,
                                                                    2 * (job0 + x) + 1, smem);
@@ -1565,8 +1575,15 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
                                                                     2 * (job0 + x) + 1, smem);
             }
         } else if (kind == 2) {
-            // head piece (or all) of dKV key tile x
+            // the short dQ job if any, then the head piece (or all) of dKV
+            // key tile x
             const int nkv = QT - x, lkv = len;
+            if (shrt != kNoShort) {
+                debug_poison<D, kDebug>(smem);
+                dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
+                                                                   shrt + 1, -1, smem);
+                unit_gap<2 * (D / 64)>();
+            }
             debug_poison<D, kDebug>(smem);
             dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(
                 a, a, b, h, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1, smem);

@@ -1,13 +1,15 @@
 // CPU check of the split plan's planner (flash-attention3_amd/csrc/fa3_split_plan.h),
 // built under ASan + UBSan: for every M the kernel can receive (2 .. 128),
-//   * each short dQ job (query tiles 0 .. M - 1) is placed exactly once, on a
-//     dKV pair's remainder workgroup or a dQ pair's head-piece workgroup;
+//   * each short dQ job (query tiles 0 .. M - 1) is placed exactly once, on
+//     one of the four workgroup kinds of a pair;
 //   * every head length lies in 1 .. the job's tile count (the kernel's
 //     descriptor holds it in 9 bits);
-//   * the planner's modelled finishing time is no later than that of the
-//     fixed pairing it replaces (dKV pair x runs short job x, dQ pairs none),
+//   * the plan's recorded makespan is its modelled finishing time, and it
+//     is no later than that of the fixed pairing the planner replaced (dKV
+//     pair x runs short job x on its remainder's workgroup, dQ pairs none),
 //     each pair at its best head length under the same model.
 // Exit status 0 when all hold.
+#include <cmath>
 #include <cstdio>
 #include <vector>
 
@@ -23,21 +25,25 @@ int main() {
         double planned = 0, fixed = 0;
         int h = 0;
         for (int x = 0; x < M; ++x) {
-            for (int s : {p.short_kv[x], p.short_q[x]}) {
+            for (int k = 0; k < 4; ++k) {
+                const int s = p.shrt[k][x];
                 if (s >= M || s < -1) ++bad;
                 else if (s >= 0) ++seen[s];
             }
             if (p.head_kv[x] < 1 || p.head_kv[x] > QT - x || p.head_kv[x] > 511) ++bad;
             if (p.head_q[x] < 1 || p.head_q[x] > M + x + 1 || p.head_q[x] > 511) ++bad;
-            planned = std::max(planned, plan_model::kv_pair(QT, x, p.short_kv[x], &h));
-            planned = std::max(planned, plan_model::q_pair(M, x, p.short_q[x], &h));
-            fixed = std::max(fixed, plan_model::kv_pair(QT, x, x, &h));
-            fixed = std::max(fixed, plan_model::q_pair(M, x, -1, &h));
+            planned = std::max(planned, plan_model::kv_pair(QT, x, p.shrt[2][x], p.shrt[1][x], &h));
+            if (h != p.head_kv[x]) ++bad;
+            planned = std::max(planned, plan_model::q_pair(M, x, p.shrt[3][x], p.shrt[0][x], &h));
+            if (h != p.head_q[x]) ++bad;
+            fixed = std::max(fixed, plan_model::kv_pair(QT, x, -1, x, &h));
+            fixed = std::max(fixed, plan_model::q_pair(M, x, -1, -1, &h));
         }
         for (int s = 0; s < M; ++s)
             if (seen[s] != 1) ++bad;
+        if (std::fabs(planned - p.makespan) > 1e-9) ++bad;
         if (planned > fixed + 1e-9) ++bad;
-        if (M == 16 || bad)
+        if (M == 8 || M == 16 || bad)
             std::printf("M=%d modelled %.2f (fixed pairing %.2f) problems so far %d\n", M, planned,
                         fixed, bad);
     }
