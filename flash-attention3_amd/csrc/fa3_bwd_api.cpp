@@ -28,13 +28,14 @@ hipError_t launch_device(hipStream_t stream, int* dev) {
     int cur = -1;
     hipError_t e = hipGetDevice(&cur);
     if (e != hipSuccess) return e;
+    hipDevice_t sd = -1;
     if (stream != nullptr) {
-        hipDevice_t sd = -1;
         e = hipStreamGetDevice(stream, &sd);
         if (e != hipSuccess) return e;
-        if ((int)sd != cur) return hipErrorInvalidDevice;
     }
-    *dev = cur;
+    const int d = launch_device_of(cur, stream != nullptr, (int)sd);
+    if (d < 0) return hipErrorInvalidDevice;
+    *dev = d;
     return hipSuccess;
 }
 }  // namespace fa3

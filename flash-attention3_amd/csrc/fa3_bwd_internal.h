@@ -24,6 +24,15 @@ constexpr int kQueueStride = 32;  // 32-bit words between counters
 constexpr int kQueueExitWord = 16;  // the launch's exit count, on queue 0's line
 constexpr size_t kQueueBytes = (size_t)kQueues * kQueueStride * 4;
 
+// The device that a launch on a stream runs on: the current device, for the
+// null stream or a stream of the current device; -1 for a stream of another
+// device (the library's per-device arrays -- the no-allocation scratch, the
+// give-up count -- are looked up with the current device, so such a launch
+// is refused rather than handed another GPU's addresses).
+inline int launch_device_of(int current, bool has_stream, int stream_device) {
+    return !has_stream || stream_device == current ? current : -1;
+}
+
 // Division by a launch-invariant divisor d (1 <= d < 2^31) of 0 <= n < 2^31
 // as a multiply-high, an add and a shift (Granlund-Montgomery round-up
 // method): with s = ceil(log2 d) and mul = floor(2^32 (2^s - d) / d) + 1,
