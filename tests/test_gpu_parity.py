@@ -168,13 +168,15 @@ def test_split_wait_failure_is_reported():
     """A split job's second piece that gives up waiting for the first piece's
     partial sums writes the launch's epoch into the workspace's error word,
     and the synchronised call returns HIP_ERROR instead of a silently wrong
-    sum.  Forced from the host: a spin limit of 0 polls makes every wait give
-    up at once, while every workgroup still runs to its end.  With the
+    sum.  Forced from the host: a spin limit of -300 makes every wait give
+    up at once and holds every first piece's publish for ~1 ms, so that
+    every wait gives up before the partial sums are there, while every
+    workgroup still runs to its end.  With the
     default limit back, the next call is correct and reports SUCCESS."""
-    log("[case] split wait gives up (spin limit 0) at P3")
+    log("[case] split wait gives up (spin limit -300) at P3")
     lib = F.load()
     g = O.golden(1, 4, 4, 2048, 128, True)
-    lib.shaobo_fa3_ext_set_split_spin_limit(0)
+    lib.shaobo_fa3_ext_set_split_spin_limit(-300)
     try:
         res = run_v2(g, torch)
     finally:

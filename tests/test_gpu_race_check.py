@@ -96,8 +96,8 @@ def _split_sync_words(ws, B, H, S):
 
 
 def test_split_giveup_visible_without_sync():
-    """A split wait that gives up in an unsynchronised call (spin limit 0,
-    sync_after_launch = 0) is reported afterwards by the workspace query and
+    """A split wait that gives up in an unsynchronised call (spin limit -300:
+    every wait gives up before the held publish; sync_after_launch = 0) is reported afterwards by the workspace query and
     counted by the GPU's give-up count; the query clears the word, so it
     reports once; the synchronisation words are all left cleared (a replay
     of a captured graph reuses the epoch and must not find a stale 'ready');
@@ -129,7 +129,7 @@ def test_split_giveup_visible_without_sync():
                                    None, ctypes.byref(p))
         assert st == F.SUCCESS, F.status_name(st)
 
-    lib.shaobo_fa3_ext_set_split_spin_limit(0)
+    lib.shaobo_fa3_ext_set_split_spin_limit(-300)  # every wait gives up before the publish
     try:
         call()
     finally:
