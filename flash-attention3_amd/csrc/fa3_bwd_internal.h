@@ -165,9 +165,7 @@ hipError_t launch_component(const BwdProblem& p, const BwdTensors& t, int role);
 size_t naive_workspace_bytes(const BwdProblem& p);
 hipError_t launch_naive(const BwdProblem& p, const BwdTensors& t, void* workspace, int role);
 
-// Polls a split wait makes before it gives up (test hook; default 1 << 24);
-// polls < 0: none, and every first piece holds its publish for -polls
-// sleeps of ~3 us (at most 4096), so that every wait gives up before it.
+// Polls a split wait makes before it gives up (test hook; default 1 << 24).
 void set_split_spin_limit(int polls);
 
 // Race-check instantiations of the main kernel for the launches that follow

@@ -60,7 +60,6 @@ FusedArgs base_args(const BwdProblem& p, const BwdTensors& t) {
 
 
 std::atomic<int> g_spin_limit{1 << 24};
-std::atomic<int> g_publish_delay{0};
 std::atomic<bool> g_debug_kernels{false};
 
 // Compute units of device `dev` (cached per device); 0 if unknown.
@@ -124,10 +123,7 @@ struct Checked {
 
 }  // namespace
 
-void set_split_spin_limit(int polls) {
-    g_spin_limit.store(polls < 0 ? 0 : polls);
-    g_publish_delay.store(polls < 0 ? (polls < -4096 ? 4096 : -polls) : 0);
-}
+void set_split_spin_limit(int polls) { g_spin_limit.store(polls < 0 ? 0 : polls); }
 
 void set_debug_kernels(bool on) { g_debug_kernels.store(on); }
 
@@ -279,7 +275,6 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     err = split_giveup_count(t.device, &a.giveups);
     if (err != hipSuccess) return err;
     a.spin_limit = g_spin_limit.load();
-    a.publish_delay = g_publish_delay.load();
     a.bal_m = plan.bal_m;
     if (plan.bal_m > 0) {
         a.n_split = plan.n_split;

@@ -147,7 +147,6 @@ struct FusedArgs {
     unsigned long long* err;  // set to epoch when a split wait gives up
     unsigned long long* giveups;  // this GPU's count of split waits that gave up
     int spin_limit;
-    int publish_delay;        // test hook: sleeps before a first piece's publish (0: none)
     int n_split;              // split jobs per role
     float* part_kv;    // [job][wave][register / 4][lane][4] fp32, first piece's sums
     float* part_q;
@@ -758,9 +757,6 @@ __device__ __forceinline__ bool split_end(const A& a, int job, FA3_LDS int* flag
     wait_vm_lgkm0<0>();
     barrier();
     if (threadIdx.x == 0) {
-        // test hook (0 outside tests): hold the publish, so that the second
-        // piece's wait surely gives up first
-        for (int i = 0; i < a.publish_delay; ++i) __builtin_amdgcn_s_sleep(127);
         unsigned long long* ready = a.sync + 2 * job + 1;
         if (__hip_atomic_exchange(ready, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
             giveup_marker(a.epoch))

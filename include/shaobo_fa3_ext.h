@@ -43,9 +43,7 @@ int shaobo_fa3_bwd_v2_on_stream(const void* dout,
  * (sync_after_launch = 1) returns SHAOBO_FA3_STATUS_HIP_ERROR (unsynchronised
  * calls: shaobo_fa3_ext_split_status / _split_error_count); 0 makes every
  * split wait give up at once (a wait that finds the partial sums already
- * published carries on, so whether a call fails depends on timing); a
- * negative value -n also holds every first piece's publish for n sleeps of
- * ~3 us (n at most 4096), so that every wait surely gives up before it.
+ * published carries on, so whether a call fails depends on timing).
  * Process-wide; affects launches made after the call. */
 void shaobo_fa3_ext_set_split_spin_limit(int polls);
 
