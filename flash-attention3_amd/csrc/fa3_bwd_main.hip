@@ -236,6 +236,18 @@ hipError_t launch_component(const BwdProblem& p, const BwdTensors& t, int role) 
     return hipGetLastError();
 }
 
+#ifdef FA3_TIMELINE
+namespace {
+unsigned long long* g_timeline = nullptr;
+}
+// Timeline build only (no product entry point): the device buffer that the
+// main-kernel launches that follow fill with per-workgroup timestamps (null:
+// none).  At least 2^21 + 32 x workgroups 64-bit words, zeroed by the caller.
+extern "C" __attribute__((visibility("default"))) void fa3_timeline_set(void* buffer) {
+    g_timeline = static_cast<unsigned long long*>(buffer);
+}
+#endif
+
 hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* workspace,
                            unsigned long long* epoch) {
     const WorkspacePlan plan = plan_workspace(p);
@@ -275,6 +287,9 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     err = split_giveup_count(t.device, &a.giveups);
     if (err != hipSuccess) return err;
     a.spin_limit = g_spin_limit.load();
+#ifdef FA3_TIMELINE
+    a.tl = g_timeline;
+#endif
     a.bal_m = plan.bal_m;
     if (plan.bal_m > 0) {
         a.n_split = plan.n_split;

@@ -152,9 +152,33 @@ struct FusedArgs {
     float* part_q;
     uint32_t part_kv_bytes;
     uint32_t part_q_bytes;
+#ifdef FA3_TIMELINE
+    unsigned long long* tl;  // per-workgroup timestamps (timeline build only, below)
+#endif
 };
 
 namespace {
+
+// Timeline build (-DFA3_TIMELINE, lib/libshaobo_fa3_bwd_timeline.so; the
+// product build compiles none of this): per workgroup, words 64 blockIdx.x ..
+// hold [0] its entry time, [29] its split descriptor, [30] HW_ID, [31]
+// XCC_ID; unit u < 4 of the workgroup stamps word (1 << 21) + 32 blockIdx.x +
+// 8 u + s with s = 0 unit start, 7 resident tiles landed, 1 loop start,
+// 2 last step done, 3 unit end (its stores complete), 4 first piece
+// published, 5 second piece past its wait, 6 partial sums added.  The stamps
+// are s_memrealtime (100 MHz) values written by the first gradient wave.
+#ifdef FA3_TIMELINE
+template <typename A>
+__device__ __forceinline__ void tl_unit(const A& a, int u, int s) {
+    if (a.tl != nullptr && threadIdx.x == 4 * kWave && u < 4)
+        a.tl[(1u << 21) + (size_t)blockIdx.x * 32 + u * 8 + s] = __builtin_amdgcn_s_memrealtime();
+}
+#define FA3_TL(u, s) tl_unit(a, u, s)
+#define FA3_TL_DRAIN() wait_vm_lgkm0<0>()
+#else
+#define FA3_TL(u, s) ((void)0)
+#define FA3_TL_DRAIN() ((void)0)
+#endif
 
 
 // The kernel arguments where the launch put them, in the kernel-argument
@@ -808,7 +832,7 @@ template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = fals
           bool kScaled = true, bool kDebug = false, typename DA>
 __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b, int hkv, int kt, int qa, int qb,
                                          int slot,
-                         FA3_LDS char* smem) {
+                         FA3_LDS char* smem, int tlu = 0) {
     static_assert(kRows == 0 || kRows == 1, "dKV rows come as -lse2/-delta or packed");
     using C = Cfg<D>;
     const int tid = opaque_tid();
@@ -1032,8 +1056,11 @@ __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b,
             score(next_masked(), s1, pwr, ld, true);
             __builtin_amdgcn_sched_barrier(0);
         };
+        FA3_TL(tlu, 0);
         prologue_loads();
+        FA3_TL(tlu, 7);
         prologue(st_ld, pds0);
+        FA3_TL(tlu, 1);
         int j = 0;
         for (; j + 2 < n_it; j += 2) {
             step(st_ld, st_1, pds1);
@@ -1125,8 +1152,11 @@ __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b,
             top();
             grad(xcur, prd);
         };
+        FA3_TL(tlu, 0);
         prologue_loads();
+        FA3_TL(tlu, 7);
         prologue(st_ld);
+        FA3_TL(tlu, 1);
         int j = 0;
         for (; j + 2 < n_it; j += 2) {
             step(st_ld, st_1, pds0, xa, xb);
@@ -1140,11 +1170,14 @@ __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b,
         } else {
             last(xa, pds0);
         }
+        FA3_TL(tlu, 2);
         // st_1 is free now: nobody reads it any more, and only the latest
         // issue (into st_ld, or st_2 after a rotate) may still be landing, so
         // it stages the outputs
         if (slot < 0) {
             store_dkv<D, kBf16>(d, b, hkv, kbase, t, lane, acc, st_1);
+            FA3_TL_DRAIN();
+            FA3_TL(tlu, 3);
             return;
         }
         // partial sums of the first piece: [job][wave][2 kPpw accumulator blocks]
@@ -1153,9 +1186,15 @@ __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b,
         const uint32_t part = (uint32_t)((slot >> 1) * 4 + t) * (kBlk * 4096);
         f32x16* flat = &acc[0][0];
         if (split_end(d, slot >> 1, flag, [&] { put_partials<kBlk>(pr, part, flat, lane); })) {
+            FA3_TL(tlu, 5);
             add_partials<kBlk>(pr, part, flat, lane);
+            FA3_TL(tlu, 6);
             store_dkv<D, kBf16>(d, b, hkv, kbase, t, lane, acc, st_1);
+        } else {
+            FA3_TL(tlu, 4);
         }
+        FA3_TL_DRAIN();
+        FA3_TL(tlu, 3);
     }
 }
 
@@ -1169,7 +1208,7 @@ template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = fals
           bool kScaled = true, bool kDebug = false, typename DA>
 __device__ __forceinline__ void dq_role(const FusedArgs& a, const DA& d, int b, int hq, int hkv, int qt, int ka,
                                         int kb, int slot,
-                        FA3_LDS char* smem) {
+                        FA3_LDS char* smem, int tlu = 0) {
     static_assert(kRows == 0 || kRows == 2, "dQ rows come as -lse2/-delta or max/sum/delta");
     using C = Cfg<D>;
     const int tid = opaque_tid();
@@ -1339,8 +1378,11 @@ __device__ __forceinline__ void dq_role(const FusedArgs& a, const DA& d, int b, 
             score(masked, s1, pwr, ld, true);
             __builtin_amdgcn_sched_barrier(0);
         };
+        FA3_TL(tlu, 0);
         prologue_loads();
+        FA3_TL(tlu, 7);
         prologue(st_ld, ds0);
+        FA3_TL(tlu, 1);
         int j = 0;
         for (; j + 2 < n_kt; j += 2) {
             step(kCausal && ka + j + 1 == qt, st_ld, st_1, ds1);
@@ -1413,8 +1455,11 @@ __device__ __forceinline__ void dq_role(const FusedArgs& a, const DA& d, int b, 
             top();
             grad(xcur, prd);
         };
+        FA3_TL(tlu, 0);
         prologue_loads();
+        FA3_TL(tlu, 7);
         prologue(st_ld);
+        FA3_TL(tlu, 1);
         int j = 0;
         for (; j + 2 < n_kt; j += 2) {
             step(st_ld, st_1, ds0, xa, xb);
@@ -1428,9 +1473,12 @@ __device__ __forceinline__ void dq_role(const FusedArgs& a, const DA& d, int b, 
         } else {
             last(xa, ds0);
         }
+        FA3_TL(tlu, 2);
         // st_1 is free now (see dkv_role) and stages the outputs
         if (slot < 0) {
             store_dq<D, kBf16>(d, q0, t, lane, acc, st_1);
+            FA3_TL_DRAIN();
+            FA3_TL(tlu, 3);
             return;
         }
         // partial sums of the first piece: [job][wave][kRb accumulator blocks]
@@ -1438,9 +1486,15 @@ __device__ __forceinline__ void dq_role(const FusedArgs& a, const DA& d, int b, 
         const uint32_t part = (uint32_t)((slot >> 1) * 4 + t) * (kRb * 4096);
         if (split_end(d, d.n_split + (slot >> 1), flag,
                       [&] { put_partials<kRb>(pr, part, acc, lane); })) {
+            FA3_TL(tlu, 5);
             add_partials<kRb>(pr, part, acc, lane);
+            FA3_TL(tlu, 6);
             store_dq<D, kBf16>(d, q0, t, lane, acc, st_1);
+        } else {
+            FA3_TL(tlu, 4);
         }
+        FA3_TL_DRAIN();
+        FA3_TL(tlu, 3);
     }
 }
 
@@ -1519,6 +1573,14 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     static_assert(!(kScaled && kSplit), "the split plan runs unscaled");
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
+#ifdef FA3_TIMELINE
+    if (a.tl != nullptr && threadIdx.x == 0) {
+        unsigned long long* p = a.tl + (size_t)blockIdx.x * 64;
+        p[0] = __builtin_amdgcn_s_memrealtime();
+        p[30] = __builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_ID
+        p[31] = __builtin_amdgcn_s_getreg((31 << 11) | 20);  // XCC_ID
+    }
+#endif
     const int group = a.group;
     const int QT = a.seqlen / 64;
     int g, pos;
@@ -1533,6 +1595,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
                          "s"(a.q_hs), "s"(a.kv_rs), "s"(a.kv_hs), "s"(a.q), "s"(a.k), "s"(a.v),
                          "s"(a.dout), "s"(a.nlse2), "s"(a.ndelta));
         const int kind = desc & 3, x = (desc >> 2) & 127, len = (desc >> 15) & 511;
+#ifdef FA3_TIMELINE
+        if (a.tl != nullptr && threadIdx.x == 0) a.tl[(size_t)blockIdx.x * 64 + 29] = desc;
+#endif
         const int shrt = desc >> 24;
         g = (desc >> 9) & 63;
         // G = 1: group g is query head g (and KV head g) of batch b
@@ -1545,19 +1610,20 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
             const int nq = M + x + 1, lq = len;
             debug_poison<D, kDebug>(smem);
             dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, M + x, M + x, QT, -1,
-                                                                smem);
+                                                                smem, 0);
             if (shrt != kNoShort) {
                 unit_gap<4 * (D / 64)>();
                 debug_poison<D, kDebug>(smem);
                 dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
-                                                                   shrt + 1, -1, smem);
+                                                                   shrt + 1, -1, smem, 1);
             }
             if (lq < nq) {
                 if (shrt != kNoShort) unit_gap<2 * (D / 64)>();
                 else unit_gap<4 * (D / 64)>();
                 debug_poison<D, kDebug>(smem);
-                dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, M + x, lq, nq,
-                                                                   2 * (job0 + x) + 1, smem);
+                dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(
+                    a, a, b, h, h, M + x, lq, nq, 2 * (job0 + x) + 1, smem,
+                    shrt != kNoShort ? 2 : 1);
             }
         } else if (kind == 1) {
             // the short dQ job (query tile shrt, whole) if any, then the
@@ -1566,13 +1632,14 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
             if (shrt != kNoShort) {
                 debug_poison<D, kDebug>(smem);
                 dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
-                                                                   shrt + 1, -1, smem);
+                                                                   shrt + 1, -1, smem, 0);
                 if (lkv < nkv) unit_gap<2 * (D / 64)>();
             }
             if (lkv < nkv) {
                 debug_poison<D, kDebug>(smem);
-                dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, x, x + lkv, QT,
-                                                                    2 * (job0 + x) + 1, smem);
+                dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(
+                    a, a, b, h, x, x + lkv, QT, 2 * (job0 + x) + 1, smem,
+                    shrt != kNoShort ? 1 : 0);
             }
         } else if (kind == 2) {
             // the short dQ job if any, then the head piece (or all) of dKV
@@ -1581,12 +1648,13 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
             if (shrt != kNoShort) {
                 debug_poison<D, kDebug>(smem);
                 dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
-                                                                   shrt + 1, -1, smem);
+                                                                   shrt + 1, -1, smem, 0);
                 unit_gap<2 * (D / 64)>();
             }
             debug_poison<D, kDebug>(smem);
             dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(
-                a, a, b, h, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1, smem);
+                a, a, b, h, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1, smem,
+                shrt != kNoShort ? 1 : 0);
         } else {
             // the short dQ job (query tile shrt, whole) if any, then the
             // head piece (or all) of dQ query tile M + x
@@ -1594,12 +1662,13 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
             if (shrt != kNoShort) {
                 debug_poison<D, kDebug>(smem);
                 dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
-                                                                   shrt + 1, -1, smem);
+                                                                   shrt + 1, -1, smem, 0);
                 unit_gap<2 * (D / 64)>();
             }
             debug_poison<D, kDebug>(smem);
             dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(
-                a, a, b, h, h, M + x, 0, min(lq, nq), lq < nq ? 2 * (job0 + x) : -1, smem);
+                a, a, b, h, h, M + x, 0, min(lq, nq), lq < nq ? 2 * (job0 + x) : -1, smem,
+                shrt != kNoShort ? 1 : 0);
         }
         return;
     }
