@@ -309,7 +309,8 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
             const int kind = pos / M, x = pos % M;
             const int len = kind == 1 || kind == 2 ? sp.head_kv[x] : sp.head_q[x];
             const int s = sp.shrt[kind][x];
-            a.split_desc[id] = split_desc(kind, x, g, len, s < 0 ? kNoShort : s);
+            const int sfield = s < 0 ? kNoShort : sp.after[kind][x] ? kShortAfter + s : s;
+            a.split_desc[id] = split_desc(kind, x, g, len, sfield);
         }
     }
     if (g_debug_kernels.load()) launch_race_check(a, p.head_dim, p.causal, p.bf16, t.stream);

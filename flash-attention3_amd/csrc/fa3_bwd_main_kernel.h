@@ -73,10 +73,13 @@ constexpr int kMaxSplitWgs = 4 * kMaxBalM;  // its workgroups: one per job
 // the host): bits 0..1 the workgroup's kind (see bwd_main_kernel), 2..8 x,
 // 9..14 the (batch, head) group, 15..23 the head-piece length of the split
 // job it works on (tiles; a length covering the whole job leaves it
-// unsplit), 24..31 the short dQ job (query tile < M) that a kind 1 or 3
-// workgroup runs first, or kNoShort.  The split plan has at most 512 jobs
-// and S / 64 >= 4, so M <= 128, groups <= 64 and lengths <= 256 fit.
+// unsplit), 24..31 the short dQ job (query tile < M) that the workgroup
+// runs before its piece (kind 0: between its whole dKV job and its dQ
+// remainder), kShortAfter + that tile for a short job run after the piece
+// (tiles < 127 only), or kNoShort.  The split plan has at most 512 jobs and
+// S / 64 >= 4, so M <= 128, groups <= 64 and lengths <= 256 fit.
 constexpr int kNoShort = 255;
+constexpr int kShortAfter = 128;
 __host__ __device__ constexpr uint32_t split_desc(int kind, int x, int g, int len, int shrt) {
     return (uint32_t)kind | ((uint32_t)x << 2) | ((uint32_t)g << 9) | ((uint32_t)len << 15) |
            ((uint32_t)shrt << 24);
@@ -1566,10 +1569,14 @@ __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int&
 // (default plan, launches with scale_log2 <= 1).  The split plan keeps them
 // unscaled: its units are short (8 to 32 steps), and the scaling in each
 // unit's prologue cost about what its steps save (P3 +0.5 %).
-// kDebug selects the race-check instantiation (see debug_sync).
-template <int D, bool kCausal, bool kBf16, bool kSplit, bool kScaled, bool kDebug = false>
+// kDebug selects the race-check instantiation (see debug_sync).  kAfter: a
+// split plan that places short jobs after pieces (only such plans run the
+// code for them).
+template <int D, bool kCausal, bool kBf16, bool kSplit, bool kScaled, bool kDebug = false,
+          bool kAfter = false>
 __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     static_assert(kCausal || !kSplit, "the split plan is causal");
+    static_assert(kSplit || !kAfter, "short jobs after pieces are a split-plan placement");
     static_assert(!(kScaled && kSplit), "the split plan runs unscaled");
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
@@ -1598,7 +1605,11 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
 #ifdef FA3_TIMELINE
         if (a.tl != nullptr && threadIdx.x == 0) a.tl[(size_t)blockIdx.x * 64 + 29] = desc;
 #endif
-        const int shrt = desc >> 24;
+        // (a plan with short jobs after pieces runs the kAfter instantiation)
+        const int sfield = desc >> 24;
+        const bool after = kAfter && sfield != kNoShort && sfield >= kShortAfter;
+        const int shrt =
+            kAfter && sfield != kNoShort ? sfield & (kShortAfter - 1) : sfield;
         g = (desc >> 9) & 63;
         // G = 1: group g is query head g (and KV head g) of batch b
         const int b = fdiv(a.div_hkv, g), h = g - b * a.heads_kv;
@@ -1606,30 +1617,30 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
         const int job0 = g * M;
         if (kind == 0) {
             // dKV key tile M + x whole, the short dQ job (query tile shrt,
-            // whole) if any, then the remainder of dQ query tile M + x
+            // whole) if placed before, then the remainder of dQ query tile M + x
             const int nq = M + x + 1, lq = len;
             debug_poison<D, kDebug>(smem);
             dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, M + x, M + x, QT, -1,
                                                                 smem, 0);
-            if (shrt != kNoShort) {
+            if (shrt != kNoShort && !after) {
                 unit_gap<4 * (D / 64)>();
                 debug_poison<D, kDebug>(smem);
                 dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
                                                                    shrt + 1, -1, smem, 1);
             }
             if (lq < nq) {
-                if (shrt != kNoShort) unit_gap<2 * (D / 64)>();
+                if (shrt != kNoShort && !after) unit_gap<2 * (D / 64)>();
                 else unit_gap<4 * (D / 64)>();
                 debug_poison<D, kDebug>(smem);
                 dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(
                     a, a, b, h, h, M + x, lq, nq, 2 * (job0 + x) + 1, smem,
-                    shrt != kNoShort ? 2 : 1);
+                    (shrt != kNoShort && !after) ? 2 : 1);
             }
         } else if (kind == 1) {
-            // the short dQ job (query tile shrt, whole) if any, then the
+            // the short dQ job (query tile shrt, whole) if placed before, then the
             // remainder of dKV key tile x
             const int nkv = QT - x, lkv = len;
-            if (shrt != kNoShort) {
+            if (shrt != kNoShort && !after) {
                 debug_poison<D, kDebug>(smem);
                 dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
                                                                    shrt + 1, -1, smem, 0);
@@ -1639,13 +1650,13 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
                 debug_poison<D, kDebug>(smem);
                 dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(
                     a, a, b, h, x, x + lkv, QT, 2 * (job0 + x) + 1, smem,
-                    shrt != kNoShort ? 1 : 0);
+                    (shrt != kNoShort && !after) ? 1 : 0);
             }
         } else if (kind == 2) {
-            // the short dQ job if any, then the head piece (or all) of dKV
+            // the short dQ job if placed before, then the head piece (or all) of dKV
             // key tile x
             const int nkv = QT - x, lkv = len;
-            if (shrt != kNoShort) {
+            if (shrt != kNoShort && !after) {
                 debug_poison<D, kDebug>(smem);
                 dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
                                                                    shrt + 1, -1, smem, 0);
@@ -1654,12 +1665,12 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
             debug_poison<D, kDebug>(smem);
             dkv_role<D, kCausal, kBf16, 0, true, false, kDebug>(
                 a, a, b, h, x, x, x + min(lkv, nkv), lkv < nkv ? 2 * (job0 + x) : -1, smem,
-                shrt != kNoShort ? 1 : 0);
+                (shrt != kNoShort && !after) ? 1 : 0);
         } else {
-            // the short dQ job (query tile shrt, whole) if any, then the
+            // the short dQ job (query tile shrt, whole) if placed before, then the
             // head piece (or all) of dQ query tile M + x
             const int nq = M + x + 1, lq = len;
-            if (shrt != kNoShort) {
+            if (shrt != kNoShort && !after) {
                 debug_poison<D, kDebug>(smem);
                 dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, b, h, h, shrt, 0,
                                                                    shrt + 1, -1, smem, 0);
@@ -1668,7 +1679,31 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
             debug_poison<D, kDebug>(smem);
             dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(
                 a, a, b, h, h, M + x, 0, min(lq, nq), lq < nq ? 2 * (job0 + x) : -1, smem,
-                shrt != kNoShort ? 1 : 0);
+                (shrt != kNoShort && !after) ? 1 : 0);
+        }
+        // a short job placed after the piece (kAfter instantiations only):
+        // it fills the time a piece that published first would wait for its
+        // partner's add.  Everything it needs is decoded again from the
+        // descriptor and read again from the arguments (the empty asm), so
+        // that nothing but the descriptor is held in scalar registers across
+        // the piece.  The gap waits as after a dQ unit: that leaves fewer
+        // stores in flight than a gap after a dKV unit allows, so it is safe
+        // after either.
+        if constexpr (kAfter) {
+            uint32_t dd = desc;
+            __asm__ volatile("" : "+s"(dd));
+            const int sa = dd >> 24;
+            if (sa != kNoShort && sa >= kShortAfter) {
+                KArgs* ap = &kargs();
+                __asm__ volatile("" : "+s"(ap));
+                const int ga = (dd >> 9) & 63;
+                const int ba = fdiv(ap->div_hkv, ga), ha = ga - ba * ap->heads_kv;
+                const int st = sa - kShortAfter;
+                unit_gap<2 * (D / 64)>();
+                debug_poison<D, kDebug>(smem);
+                dq_role<D, kCausal, kBf16, 0, true, false, kDebug>(a, a, ba, ha, ha, st, 0, st + 1,
+                                                                   -1, smem, 3);
+            }
         }
         return;
     }
@@ -1770,17 +1805,26 @@ void launch_dd(const FusedArgs& a, bool causal, bool bf16, hipStream_t stream) {
     const dim3 grid(a.persist > 0 ? a.persist : a.n_groups * a.jobs_per_group);
     const dim3 block(kThreads);
     const bool split = a.bal_m > 0;  // causal only (plan_workspace)
+    // the split plan's instantiation with the code for short jobs after
+    // pieces, when the plan places one there
+    bool after = false;
+    for (int i = 0; split && i < a.n_jobs; ++i) {
+        const int sf = (int)(a.split_desc[i] >> 24);
+        after = after || (sf != kNoShort && sf >= kShortAfter);
+    }
     // K c / Q c cannot overflow fp16 when c <= 1
     const bool scaled = a.scale_log2 <= 1.f;
     auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream, a); };
     if (bf16) {
-        if (split) go(bwd_main_kernel<D, true, true, true, false, kDebug>);
+        if (split) go(after ? bwd_main_kernel<D, true, true, true, false, kDebug, true>
+                            : bwd_main_kernel<D, true, true, true, false, kDebug, false>);
         else if (causal) go(scaled ? bwd_main_kernel<D, true, true, false, true, kDebug>
                                    : bwd_main_kernel<D, true, true, false, false, kDebug>);
         else go(scaled ? bwd_main_kernel<D, false, true, false, true, kDebug>
                        : bwd_main_kernel<D, false, true, false, false, kDebug>);
     } else {
-        if (split) go(bwd_main_kernel<D, true, false, true, false, kDebug>);
+        if (split) go(after ? bwd_main_kernel<D, true, false, true, false, kDebug, true>
+                            : bwd_main_kernel<D, true, false, true, false, kDebug, false>);
         else if (causal) go(scaled ? bwd_main_kernel<D, true, false, false, true, kDebug>
                                    : bwd_main_kernel<D, true, false, false, false, kDebug>);
         else go(scaled ? bwd_main_kernel<D, false, false, false, true, kDebug>

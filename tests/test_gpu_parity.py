@@ -42,6 +42,7 @@ CASES = [
     (1, 3, 3, 384, 128, True),    # odd M = 3, 3 groups (no XCD-aligned map)
     (2, 2, 2, 1024, 128, True),   # batch 2: 4 groups
     (1, 5, 5, 640, 64, True),     # M = 5, D = 64
+    (1, 2, 2, 1536, 128, True),   # M = 12: short jobs after the pieces of kinds 1 and 2
     (1, 2, 2, 4096, 64, True),    # M = 32, D = 64
     (1, 8, 8, 2048, 64, True),    # 512 jobs: the largest split plan
     (1, 9, 9, 2048, 64, True),    # 576 jobs: causal, one head per group, default plan
