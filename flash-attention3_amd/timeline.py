@@ -86,8 +86,21 @@ def record(cfg, launches=3):
     return rows[:n_wg], raw[UNIT_BASE:UNIT_BASE + 32 * n_wg].reshape(n_wg, 4, 8), same
 
 
+def in_order(units):
+    """Each workgroup's recorded units in the order they ran (by start stamp):
+    [workgroup, position, stamp], zero where a workgroup ran fewer units (a
+    short job after a piece records in slot 3, whatever ran before it)."""
+    out = np.zeros_like(units)
+    for w in range(len(units)):
+        ran = [u for u in range(units.shape[1]) if units[w, u, S_START] > 0]
+        for i, u in enumerate(sorted(ran, key=lambda u: units[w, u, S_START])):
+            out[w, i] = units[w, u]
+    return out
+
+
 def summary(cfg, rows, units, same):
     us = lambda a, b: np.where((a > 0) & (b > 0), (a - b) / 100.0, np.nan)  # noqa: E731
+    units = in_order(units)
     ent = rows[:, 0]
     t0 = ent.min()
     kind = rows[:, 29] & 3
@@ -96,11 +109,12 @@ def summary(cfg, rows, units, same):
     out = [f"Workgroups {len(rows)}; last unit end {np.nanmax(end):.2f} µs after the first "
            f"entry (median workgroup {np.nanmedian(end):.2f}); instrumented outputs bit-equal "
            f"to the same library's uninstrumented launch: {same}.", "",
-           "Per unit, medians over the workgroups that run it (µs):", "",
+           "Per unit (in the order a workgroup runs them), medians over the workgroups that "
+           "run it (µs):", "",
            "| unit | workgroups | before the unit (entry or gap) | resident tiles landed | "
            "first phase to loop start | loop | last step to unit end |",
            "|---|---|---|---|---|---|---|"]
-    for u in range(3):
+    for u in range(units.shape[1]):
         m = units[:, u, S_START] > 0
         if not m.any():
             continue
@@ -122,6 +136,12 @@ def summary(cfg, rows, units, same):
                 f"({int(first.sum())} pieces); second piece, last step to past its wait "
                 f"{np.nanmedian(wait):.2f}, partial sums added {np.nanmedian(add):.2f}, "
                 f"converted and stored {np.nanmedian(store):.2f} ({int(second.sum())} pieces)."]
+    if rows[:, 29].any():  # split plan: the workgroup kinds' ends
+        out += ["", "Workgroup ends by split-plan kind (µs after the first entry, "
+                "min / median / max): " +
+                "; ".join(f"kind {k} {np.nanmin(end[kind == k]):.2f} / "
+                          f"{np.nanmedian(end[kind == k]):.2f} / {np.nanmax(end[kind == k]):.2f}"
+                          for k in range(4) if (kind == k).any()) + "."]
     out += ["", "The 12 workgroups that end last (kind, end µs; per unit: before, resident, "
             "first phase, loop, end):", "", "```"]
     for w in np.argsort(-np.nan_to_num(end, nan=-1.0))[:12]:
