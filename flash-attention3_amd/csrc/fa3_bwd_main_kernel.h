@@ -1539,10 +1539,18 @@ __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int&
 // the shape allows, block id -> (xcd, position) is arranged so that each XCD
 // runs whole parts of groups, keeping a head's tiles in one L2.
 //
-// Default plan: within a group, position p = (level L, slot r) with G + 1
-// slots per level: slot 0 is the dKV job of key tile L, slot r > 0 the dQ
-// job of query head r - 1 at query tile QT - 1 - L, so the dispatch order is
-// longest first (causal).
+// Default plan: the order of a group's jobs is longest first, so that the
+// short jobs come last and even out the workgroups' finishing times (list
+// scheduling).  Non-causal, or G > 1: positions p < QT are the dKV jobs of
+// key tiles p, then p = QT + G L + r the dQ job of query head r at query
+// tile QT - 1 - L -- a dKV job streams G heads' tiles and a dQ step is ~0.75
+// of a dKV step, so every dKV job is at least as long as any dQ job but the
+// causal tail (A/B against the level order below: P4 -2.2 to -2.8 %, P5
+// -0.7 to -1.0 %, B2 Hq32 Hkv8 S4096 full -6.2 %).  Causal with G = 1 (the
+// kLevels instantiations): level L holds the dKV job of key tile L (p =
+// 2 L) and the dQ job of query tile QT - 1 - L (p = 2 L + 1), two lists of
+// the same slope merged (the role order measured +0.8 to +1.7 % there, B1
+// H16 S8192 D128, and a runtime choice inside one instantiation +0.8 %).
 //
 // Split plan (bal_m = M = QT / 2 > 0; causal, G = 1, few jobs): the causal
 // jobs run 1 .. QT steps, so one long job would set the kernel's length.
@@ -1571,12 +1579,14 @@ __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int&
 // unit's prologue cost about what its steps save (P3 +0.5 %).
 // kDebug selects the race-check instantiation (see debug_sync).  kAfter: a
 // split plan that places short jobs after pieces (only such plans run the
-// code for them).
+// code for them).  kLevels: the default plan's level-by-level job order
+// (causal, G = 1; see the job map).
 template <int D, bool kCausal, bool kBf16, bool kSplit, bool kScaled, bool kDebug = false,
-          bool kAfter = false>
+          bool kAfter = false, bool kLevels = false>
 __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     static_assert(kCausal || !kSplit, "the split plan is causal");
     static_assert(kSplit || !kAfter, "short jobs after pieces are a split-plan placement");
+    static_assert(!(kSplit && kLevels), "the level order is a default-plan order");
     static_assert(!(kScaled && kSplit), "the split plan runs unscaled");
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
@@ -1711,8 +1721,20 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     // read the rest from a
     auto run = [&](KArgs& d, int id) {
         job_of(d, id, g, pos);
-        const int level = fdiv(d.div_g1, pos);
-        const int slot = pos - level * (group + 1);
+        // the job's level (key tile of a dKV job; a dQ job's query tile is
+        // QT - 1 - level) and slot (0: dKV, r > 0: dQ of query head r - 1)
+        int level, slot;
+        if constexpr (kLevels) {
+            level = fdiv(d.div_g1, pos);
+            slot = pos - level * (group + 1);
+        } else if (pos < QT) {
+            level = pos;
+            slot = 0;
+        } else {
+            const int r = pos - QT;
+            level = fdiv(d.div_group, r);
+            slot = 1 + r - level * group;
+        }
         const int b = fdiv(d.div_hkv, g), hkv = g - b * a.heads_kv;
         debug_poison<D, kDebug>(smem);
         if (slot == 0) {
@@ -1815,9 +1837,14 @@ void launch_dd(const FusedArgs& a, bool causal, bool bf16, hipStream_t stream) {
     // K c / Q c cannot overflow fp16 when c <= 1
     const bool scaled = a.scale_log2 <= 1.f;
     auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream, a); };
+    // the default plan's job order: level by level for causal with G = 1
+    const bool levels = causal && a.group == 1;
     if (bf16) {
         if (split) go(after ? bwd_main_kernel<D, true, true, true, false, kDebug, true>
                             : bwd_main_kernel<D, true, true, true, false, kDebug, false>);
+        else if (causal && levels)
+            go(scaled ? bwd_main_kernel<D, true, true, false, true, kDebug, false, true>
+                      : bwd_main_kernel<D, true, true, false, false, kDebug, false, true>);
         else if (causal) go(scaled ? bwd_main_kernel<D, true, true, false, true, kDebug>
                                    : bwd_main_kernel<D, true, true, false, false, kDebug>);
         else go(scaled ? bwd_main_kernel<D, false, true, false, true, kDebug>
@@ -1825,6 +1852,9 @@ void launch_dd(const FusedArgs& a, bool causal, bool bf16, hipStream_t stream) {
     } else {
         if (split) go(after ? bwd_main_kernel<D, true, false, true, false, kDebug, true>
                             : bwd_main_kernel<D, true, false, true, false, kDebug, false>);
+        else if (causal && levels)
+            go(scaled ? bwd_main_kernel<D, true, false, false, true, kDebug, false, true>
+                      : bwd_main_kernel<D, true, false, false, false, kDebug, false, true>);
         else if (causal) go(scaled ? bwd_main_kernel<D, true, false, false, true, kDebug>
                                    : bwd_main_kernel<D, true, false, false, false, kDebug>);
         else go(scaled ? bwd_main_kernel<D, false, false, false, true, kDebug>

@@ -30,12 +30,13 @@ def test_shipped_kernels_present(gated):
     for want in EXPECTED:
         assert any(want in n for n in names), want
     # every (head dim, causal, bf16) instantiation of the main kernel with
-    # scaled and unscaled resident operands, and the split-plan
-    # instantiations of the causal ones (unscaled only), without and with
-    # the code for short jobs after pieces: 24, each with its race-check twin
+    # scaled and unscaled resident operands (the causal ones also in the
+    # level-by-level job order), and the split-plan instantiations of the
+    # causal ones (unscaled only), without and with the code for short jobs
+    # after pieces: 32, each with its race-check twin
     # (shaobo_fa3_ext_set_race_check), which the gate holds to the same
     # budget
-    assert sum("bwd_main_kernel" in n for n in names) == 48
+    assert sum("bwd_main_kernel" in n for n in names) == 64
 
 
 def test_main_kernel_two_waves_per_simd(gated):
