@@ -65,6 +65,8 @@ def test_v2_matches_oracle(B, Hq, Hkv, S, D, causal):
     (1, 4, 2, 384, 128, True, 0.69),   # just below ln 2: operands scaled by c = 0.995
     (2, 4, 2, 256, 64, False, 0.02),   # small c, scaled
     (1, 1, 1, 256, 128, True, 1.0),    # split plan (unscaled at every scale)
+    (1, 1, 1, 128, 128, True, 1.0),    # level-order default plan (causal, G = 1), unscaled
+    (1, 9, 9, 2048, 64, True, 1.0),    # ... persistent (576 jobs), unscaled
 ])
 def test_v2_softmax_scales(B, Hq, Hkv, S, D, causal, scale):
     """The default plan's score waves multiply their resident operand (K, or
