@@ -202,10 +202,16 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
         dv == nullptr) {
         return SHAOBO_FA3_STATUS_INVALID_VALUE;
     }
-    const fa3::BwdProblem pr = problem_of(params);
-    const fa3::WorkspacePlan plan = fa3::plan_workspace(pr);
+    fa3::BwdProblem pr = problem_of(params);
+    fa3::WorkspacePlan plan = fa3::plan_workspace(pr);
     void* workspace = params->workspace;
     if (opt.no_alloc) {
+        // the head-split plan's per-query-head dK / dV need not fit the
+        // scratch array: then the plan with one dKV job per KV head
+        if (plan.ok && plan.head_split && plan.total > fa3::kNoAllocScratchBytes) {
+            pr.no_head_split = true;
+            plan = fa3::plan_workspace(pr);
+        }
         // shapes whose workspace exceeds the scratch array are refused
         // before any HIP call
         if (!plan.ok || plan.total > fa3::kNoAllocScratchBytes) {

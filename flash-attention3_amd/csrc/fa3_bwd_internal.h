@@ -76,6 +76,7 @@ struct BwdProblem {
     bool out_f32 = false;  // outputs fp32 (component entries) instead of fp16
     bool bf16 = false;     // 16-bit tensors are bf16 (fp16 otherwise)
     bool bshd = false;     // tensors are [B, S, H, D] (BHSD otherwise); rows stay [B, Hq, S]
+    bool no_head_split = false;  // GQA: one dKV job per KV head, whatever the shape
 };
 
 struct BwdTensors {
@@ -129,6 +130,8 @@ struct WorkspacePlan {
     size_t sync_off = 0;
     size_t pkv_off = 0;     // dKV pieces' partial sums
     size_t pq_off = 0;      // dQ pieces' partial sums
+    bool head_split = false;  // head-split default plan (GQA, few groups)
+    size_t hsd_off = 0;       // its fp32 dK contributions [B][Hq][S][D], then dV's
     size_t total = 0;
     bool ok = false;        // false: the sizes overflow size_t / the kernel's offsets
 };

@@ -180,6 +180,19 @@ hipError_t split_giveup_count(int dev, unsigned long long** ptr) {
     return e;
 }
 
+// The CU count the head-split decision assumes (an MI355X's): the plan, and
+// so the workspace size, depends on the shape only.
+constexpr int kHeadSplitCus = 256;
+// The head-split plan runs each step of a CU's share ~10 % slower (the
+// per-head fp32 dK / dV and their reduction), and a long merged job runs
+// ~10-20 % faster than the average step once few others share its CU: it
+// pays from a merged job 1.4 x the share (B4 Hq32 Hkv1 S4096 D128 causal,
+// 1.125 x: +6.5 %; B1 Hq8 Hkv2, 2.25 x: -37 %).
+constexpr double kHeadSplitMargin = 1.4;
+// ... and the shortest merged dKV job it splits: below this, the saving is
+// less than the reduction kernel's launch.
+constexpr int kHeadSplitMinSteps = 32;
+
 WorkspacePlan plan_workspace(const BwdProblem& p) {
     WorkspacePlan w;
     if (p.batch <= 0 || p.heads_q <= 0 || p.seqlen <= 0 || p.head_dim <= 0) return w;
@@ -210,6 +223,21 @@ WorkspacePlan plan_workspace(const BwdProblem& p) {
         at = at.add((size_t)w.n_split * q_piece).align();
         // the kernel addresses the partial sums with 32-bit buffer offsets
         if (w.pq_off - w.pkv_off > 0xFFFFFFFFull || at.v - w.pq_off > 0xFFFFFFFFull) return w;
+    }
+    // Head-split default plan for GQA: when one dKV job (G heads' query
+    // tiles against one key tile) is much longer than a CU's share of the
+    // work, it alone sets the kernel's length (MQA at batch 1), so each dKV
+    // job runs for one query head and the G fp32 contributions are summed
+    // afterwards.  Work in dKV steps, a dQ step ~0.75 of one.
+    const int group = p.heads_kv > 0 ? p.heads_q / p.heads_kv : 0;
+    if (w.bal_m == 0 && group > 1 && qt > 0 && !p.out_f32 && !p.no_head_split) {
+        const double steps = p.causal ? 0.5 * qt * (qt + 1.0) : (double)qt * qt;
+        const double share = (double)p.batch * p.heads_q * steps * 1.75 / kHeadSplitCus;
+        if ((double)group * qt > kHeadSplitMargin * share && group * qt >= kHeadSplitMinSteps) {
+            w.head_split = true;
+            w.hsd_off = at.v;
+            at = at.add(rows.mul((size_t)p.head_dim * sizeof(float) * 2).v).align();
+        }
     }
     if (!at.ok || !rows.ok || rows.v > (size_t)INT32_MAX) return w;
     w.total = at.v;
@@ -272,7 +300,13 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     a.nlse2 = nlse2;
     a.ndelta = ndelta;
     const int group = p.heads_q / p.heads_kv;
-    a.jobs_per_group = (p.seqlen / kTileN) * (1 + group);
+    // head split: G dKV jobs (one per query head) and G dQ jobs per key
+    // tile / query tile
+    a.jobs_per_group = (p.seqlen / kTileN) * (plan.head_split ? 2 * group : 1 + group);
+    if (plan.head_split) {
+        a.part_dk = reinterpret_cast<float*>(ws + plan.hsd_off);
+        a.part_dv = a.part_dk + (size_t)p.batch * p.heads_q * p.seqlen * p.head_dim;
+    }
     set_job_map(a);
     a.n_jobs = a.n_groups * a.jobs_per_group;
     a.queue = queue;
@@ -317,6 +351,19 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     else if (p.head_dim == 128) launch_dd<128, false>(a, p.causal, p.bf16, t.stream);
     else launch_dd<64, false>(a, p.causal, p.bf16, t.stream);
     err = hipGetLastError();
+    if (err == hipSuccess && plan.head_split) {
+        const dim3 rg((unsigned)((p.seqlen * (p.head_dim / 4) + 255) / 256),
+                      (unsigned)(p.batch * p.heads_kv));
+        _Float16* dk = static_cast<_Float16*>(t.dk);
+        _Float16* dv = static_cast<_Float16*>(t.dv);
+        auto reduce = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, rg, dim3(256), 0, t.stream, a.part_dk, a.part_dv, dk, dv,
+                               p.heads_kv, group, p.seqlen, a.kv_rs, a.kv_hs);
+        };
+        if (p.head_dim == 128) reduce(p.bf16 ? gqa_reduce_kernel<128, true> : gqa_reduce_kernel<128, false>);
+        else reduce(p.bf16 ? gqa_reduce_kernel<64, true> : gqa_reduce_kernel<64, false>);
+        err = hipGetLastError();
+    }
     return err == hipSuccess ? mark(2) : err;
 }
 

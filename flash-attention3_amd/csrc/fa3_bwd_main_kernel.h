@@ -61,6 +61,8 @@
 // so that the two halves build in parallel.
 #pragma once
 
+#include <type_traits>
+
 #include "fa3_bwd_device.h"
 #include "fa3_bwd_internal.h"
 #include "fa3_split_plan.h"
@@ -155,6 +157,12 @@ struct FusedArgs {
     float* part_q;
     uint32_t part_kv_bytes;
     uint32_t part_q_bytes;
+    // Head-split default plan (GQA with few groups): each dKV job covers one
+    // query head and writes its fp32 dK / dV contribution to
+    // part_dk / part_dv [B][Hq][S][D]; a reduce launch sums each KV head's G
+    // contributions (gqa_reduce_kernel).
+    float* part_dk;
+    float* part_dv;
 #ifdef FA3_TIMELINE
     unsigned long long* tl;  // per-workgroup timestamps (timeline build only, below)
 #endif
@@ -533,6 +541,20 @@ __device__ __forceinline__ int stage64_row(int j, int lane) {
     return ((lane >> 2) & 7) | ((j & 1) << 3) | (((lane >> 5) & 1) << 4) | ((j >> 1) << 5);
 }
 
+// The head-split plan's fp32 dK / dV contributions [B][Hq][S][D], as seen by
+// store_dkv (its fp32 path): one "KV head" per query head, rows of D.
+template <int D>
+struct PartView {
+    float* dk;
+    float* dv;
+    float scale;
+    int seqlen;
+    int heads_kv;  // the query heads
+    size_t kv_hs;  // seqlen * D
+    static constexpr int out_f32 = 1;
+    static constexpr int kv_rs = D;
+};
+
 // dV^T / dK^T accumulators of gradient wave t (pairs dkv_pair(t, u)) to dV /
 // dK of KV head hkv of batch b, keys kbase ..; lane: key 32 kb + l32,
 // d = 32 slice + 8 (i / 4) + 4 h + i % 4.  The wave's pairs share one matrix
@@ -828,14 +850,15 @@ __device__ __forceinline__ void debug_poison(FA3_LDS char* smem) {
 // dKV role
 // ----------------------------------------------------------------------------
 // Key tile kt of KV head hkv in batch b.  Streams query tiles [qa, qb) of
-// every query head of the group.  slot < 0:
+// every query head of the group (kHeadSplit: of query head hr only, the
+// outputs being that head's fp32 contribution in part_dk / part_dv).  slot < 0:
 // the job is whole and writes dK / dV; otherwise the unit is piece slot & 1
 // of split job slot >> 1 and the pieces' partial sums meet in split_end.
 template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false,
-          bool kScaled = true, bool kDebug = false, typename DA>
+          bool kScaled = true, bool kDebug = false, bool kHeadSplit = false, typename DA>
 __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b, int hkv, int kt, int qa, int qb,
                                          int slot,
-                         FA3_LDS char* smem, int tlu = 0) {
+                         FA3_LDS char* smem, int tlu = 0, int hr = 0) {
     static_assert(kRows == 0 || kRows == 1, "dKV rows come as -lse2/-delta or packed");
     using C = Cfg<D>;
     const int tid = opaque_tid();
@@ -848,7 +871,7 @@ __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b,
     const int QT = S / 64;
     const int group = d.group;
     const int kbase = kt * 64;
-    const int n_it = group * (qb - qa);
+    const int n_it = (kHeadSplit ? 1 : group) * (qb - qa);
 
     // loader index of this wave when it loads (see Cfg::kGradLoads)
     const int ldr = C::kGradLoads ? t : w;
@@ -871,7 +894,7 @@ __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b,
     // issues the same loads.  (The cursor keeps running element and
     // statistics-row offsets, so a step's issue is a few adds.)
     int ld_qt = qa, ld_left = n_it;
-    const int h0 = hkv * group;
+    const int h0 = kHeadSplit ? hr : hkv * group;
     size_t ld_e = q_elem<D>(d, b, h0, qa * 64);                  // Q / dO element
     size_t ld_row = ((size_t)b * d.heads_q + h0) * S + qa * 64;  // statistics row
     const size_t step_e = (size_t)64 * d.q_rs;
@@ -1177,6 +1200,14 @@ __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b,
         // st_1 is free now: nobody reads it any more, and only the latest
         // issue (into st_ld, or st_2 after a rotate) may still be landing, so
         // it stages the outputs
+        if (kHeadSplit) {
+            const PartView<D> pv{a.part_dk, a.part_dv, a.scale, d.seqlen, d.heads_q,
+                                 (size_t)d.seqlen * D};
+            store_dkv<D, kBf16>(pv, b, hr, kbase, t, lane, acc, st_1);
+            FA3_TL_DRAIN();
+            FA3_TL(tlu, 3);
+            return;
+        }
         if (slot < 0) {
             store_dkv<D, kBf16>(d, b, hkv, kbase, t, lane, acc, st_1);
             FA3_TL_DRAIN();
@@ -1547,10 +1578,16 @@ __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int&
 // of a dKV step, so every dKV job is at least as long as any dQ job but the
 // causal tail (A/B against the level order below: P4 -2.2 to -2.8 %, P5
 // -0.7 to -1.0 %, B2 Hq32 Hkv8 S4096 full -6.2 %).  Causal with G = 1 (the
-// kLevels instantiations): level L holds the dKV job of key tile L (p =
+// kOrder 1 instantiations): level L holds the dKV job of key tile L (p =
 // 2 L) and the dQ job of query tile QT - 1 - L (p = 2 L + 1), two lists of
 // the same slope merged (the role order measured +0.8 to +1.7 % there, B1
 // H16 S8192 D128, and a runtime choice inside one instantiation +0.8 %).
+//
+// Head-split default plan (part_dk set; GQA with so few groups that one dKV
+// job, G QT steps, would outlast the average workgroup): the dKV jobs come
+// one per query head, p = G L + r for key tile L and head r, each writing
+// its head's fp32 contribution to dK / dV; gqa_reduce_kernel then sums the
+// G contributions of each KV head in head order (deterministic).
 //
 // Split plan (bal_m = M = QT / 2 > 0; causal, G = 1, few jobs): the causal
 // jobs run 1 .. QT steps, so one long job would set the kernel's length.
@@ -1579,14 +1616,15 @@ __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int&
 // unit's prologue cost about what its steps save (P3 +0.5 %).
 // kDebug selects the race-check instantiation (see debug_sync).  kAfter: a
 // split plan that places short jobs after pieces (only such plans run the
-// code for them).  kLevels: the default plan's level-by-level job order
-// (causal, G = 1; see the job map).
+// code for them).  kOrder: the default plan's job order (see the job map) --
+// 0 dKV jobs first, 1 level by level (causal, G = 1), 2 dKV jobs first, one
+// per query head (head split).
 template <int D, bool kCausal, bool kBf16, bool kSplit, bool kScaled, bool kDebug = false,
-          bool kAfter = false, bool kLevels = false>
+          bool kAfter = false, int kOrder = 0>
 __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     static_assert(kCausal || !kSplit, "the split plan is causal");
     static_assert(kSplit || !kAfter, "short jobs after pieces are a split-plan placement");
-    static_assert(!(kSplit && kLevels), "the level order is a default-plan order");
+    static_assert(!kSplit || kOrder == 0, "the job orders are default-plan orders");
     static_assert(!(kScaled && kSplit), "the split plan runs unscaled");
     __shared__ __attribute__((aligned(1024))) char smem_raw[Cfg<D>::kBytes];
     FA3_LDS char* smem = (FA3_LDS char*)smem_raw;
@@ -1723,23 +1761,33 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
         job_of(d, id, g, pos);
         // the job's level (key tile of a dKV job; a dQ job's query tile is
         // QT - 1 - level) and slot (0: dKV, r > 0: dQ of query head r - 1)
-        int level, slot;
-        if constexpr (kLevels) {
+        int level, slot, hl = 0;  // hl: the dKV job's query head within the group (kOrder 2)
+        if constexpr (kOrder == 1) {
             level = fdiv(d.div_g1, pos);
             slot = pos - level * (group + 1);
-        } else if (pos < QT) {
-            level = pos;
-            slot = 0;
         } else {
-            const int r = pos - QT;
-            level = fdiv(d.div_group, r);
-            slot = 1 + r - level * group;
+            // dKV jobs first: QT of them (kOrder 2: G per level, one per
+            // query head), then G dQ jobs per level
+            const int n_dkv = kOrder == 2 ? group * QT : QT;
+            if (pos < n_dkv) {
+                if constexpr (kOrder == 2) {
+                    level = fdiv(d.div_group, pos);
+                    hl = pos - level * group;
+                } else {
+                    level = pos;
+                }
+                slot = 0;
+            } else {
+                const int r = pos - n_dkv;
+                level = fdiv(d.div_group, r);
+                slot = 1 + r - level * group;
+            }
         }
         const int b = fdiv(d.div_hkv, g), hkv = g - b * a.heads_kv;
         debug_poison<D, kDebug>(smem);
         if (slot == 0) {
-            dkv_role<D, kCausal, kBf16, 0, false, kScaled, kDebug>(
-                a, d, b, hkv, level, kCausal ? level : 0, QT, -1, smem);
+            dkv_role<D, kCausal, kBf16, 0, false, kScaled, kDebug, kOrder == 2>(
+                a, d, b, hkv, level, kCausal ? level : 0, QT, -1, smem, 0, hkv * group + hl);
         } else {
             const int qt = QT - 1 - level;
             dq_role<D, kCausal, kBf16, 0, false, kScaled, kDebug>(
@@ -1820,6 +1868,38 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_component_kernel(FusedArgs a)
     }
 }
 
+// Head-split plan: dK / dV of KV head hkv = the sum, in query-head order,
+// of the fp32 contributions part[b][hkv G + r][:][:] of its G query heads,
+// rounded once to the outputs' type.  Block (x, bh): 1024 elements of
+// KV head bh = b Hkv + hkv, four per thread.  HBM-bound: reads G fp32
+// values per 16-bit value written, for dK and dV.
+template <int D, bool kBf16>
+__global__ __launch_bounds__(256) void gqa_reduce_kernel(
+    const float* __restrict__ part_dk, const float* __restrict__ part_dv, _Float16* __restrict__ dk,
+    _Float16* __restrict__ dv, int heads_kv, int group, int seqlen, int kv_rs, int kv_hs) {
+    const int i = blockIdx.x * 256 + threadIdx.x;  // 4-element chunk of the head
+    if (i >= seqlen * (D / 4)) return;
+    const int bh = blockIdx.y;
+    const int b = bh / heads_kv, hkv = bh - b * heads_kv;
+    const int sq = i / (D / 4), c = i % (D / 4);
+    const size_t head = (size_t)seqlen * D;
+    const size_t src = (size_t)bh * group * head + 4 * (size_t)i;
+    f32x4 sk = *(const f32x4*)(part_dk + src), sv = *(const f32x4*)(part_dv + src);
+    for (int r = 1; r < group; ++r) {
+        sk += *(const f32x4*)(part_dk + src + r * head);
+        sv += *(const f32x4*)(part_dv + src + r * head);
+    }
+    const size_t dst = (size_t)b * heads_kv * head + (size_t)hkv * kv_hs + (size_t)sq * kv_rs + 4 * c;
+    f16x4 ok, ov;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        ok[e] = to16<kBf16>(sk[e]);
+        ov[e] = to16<kBf16>(sv[e]);
+    }
+    *(f16x4*)(dk + dst) = ok;
+    *(f16x4*)(dv + dst) = ov;
+}
+
 // Instantiation of the main kernel for a launch: head dim, causal, 16-bit
 // type, split plan, scaled resident operands, race check.
 template <int D, bool kDebug>
@@ -1837,28 +1917,37 @@ void launch_dd(const FusedArgs& a, bool causal, bool bf16, hipStream_t stream) {
     // K c / Q c cannot overflow fp16 when c <= 1
     const bool scaled = a.scale_log2 <= 1.f;
     auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream, a); };
-    // the default plan's job order: level by level for causal with G = 1
-    const bool levels = causal && a.group == 1;
-    if (bf16) {
-        if (split) go(after ? bwd_main_kernel<D, true, true, true, false, kDebug, true>
-                            : bwd_main_kernel<D, true, true, true, false, kDebug, false>);
-        else if (causal && levels)
-            go(scaled ? bwd_main_kernel<D, true, true, false, true, kDebug, false, true>
-                      : bwd_main_kernel<D, true, true, false, false, kDebug, false, true>);
-        else if (causal) go(scaled ? bwd_main_kernel<D, true, true, false, true, kDebug>
-                                   : bwd_main_kernel<D, true, true, false, false, kDebug>);
-        else go(scaled ? bwd_main_kernel<D, false, true, false, true, kDebug>
-                       : bwd_main_kernel<D, false, true, false, false, kDebug>);
+    // the default plan's job order: 2 head split (the plan set part_dk), 1
+    // level by level (causal, G = 1), else 0
+    const int order = a.part_dk != nullptr ? 2 : causal && a.group == 1 ? 1 : 0;
+    auto dflt = [&](auto bf, auto cz) {
+        constexpr bool kB = decltype(bf)::value, kC = decltype(cz)::value;
+        auto pick = [&](auto ord) {
+            constexpr int kO = decltype(ord)::value;
+            go(scaled ? bwd_main_kernel<D, kC, kB, false, true, kDebug, false, kO>
+                      : bwd_main_kernel<D, kC, kB, false, false, kDebug, false, kO>);
+        };
+        if (order == 2) pick(std::integral_constant<int, 2>{});
+        else if constexpr (kC) {
+            if (order == 1) pick(std::integral_constant<int, 1>{});
+            else pick(std::integral_constant<int, 0>{});
+        } else {
+            pick(std::integral_constant<int, 0>{});
+        }
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    if (split) {
+        if (bf16) go(after ? bwd_main_kernel<D, true, true, true, false, kDebug, true>
+                           : bwd_main_kernel<D, true, true, true, false, kDebug, false>);
+        else go(after ? bwd_main_kernel<D, true, false, true, false, kDebug, true>
+                      : bwd_main_kernel<D, true, false, true, false, kDebug, false>);
+    } else if (bf16) {
+        if (causal) dflt(T{}, T{});
+        else dflt(T{}, F{});
     } else {
-        if (split) go(after ? bwd_main_kernel<D, true, false, true, false, kDebug, true>
-                            : bwd_main_kernel<D, true, false, true, false, kDebug, false>);
-        else if (causal && levels)
-            go(scaled ? bwd_main_kernel<D, true, false, false, true, kDebug, false, true>
-                      : bwd_main_kernel<D, true, false, false, false, kDebug, false, true>);
-        else if (causal) go(scaled ? bwd_main_kernel<D, true, false, false, true, kDebug>
-                                   : bwd_main_kernel<D, true, false, false, false, kDebug>);
-        else go(scaled ? bwd_main_kernel<D, false, false, false, true, kDebug>
-                       : bwd_main_kernel<D, false, false, false, false, kDebug>);
+        if (causal) dflt(F{}, T{});
+        else dflt(F{}, F{});
     }
 }
 

@@ -223,6 +223,38 @@ def test_workspace_sizes(lib):
     assert ws(batch=1, seqlen=128, heads_q=1) == plain_bytes(1, 1, 128)
 
 
+def test_head_split_workspace_sizes(lib):
+    """GQA shapes where one dKV job over all G query heads of a KV head (G QT
+    steps) would be over 1.4 x a CU's share of the work (256 CUs, a dQ step
+    0.75 of a dKV step) and at least 32 steps take the head-split plan: the
+    plain workspace plus fp32 dK and dV per query head (2 B Hq S D x 4
+    bytes).  The decision depends on the shape only."""
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+
+    def ws(**kw):
+        p = F.make_params(lib, **kw)
+        return lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
+
+    def hs(B, Hq, S, D):
+        return plain_bytes(B, Hq, S) + align(2 * B * Hq * S * D * 4)
+    # MQA at batch 1: a dKV job of 32 x 64 steps against a share of 455
+    assert ws(batch=1, seqlen=4096, heads_q=32, heads_kv=1) == hs(1, 32, 4096, 128)
+    assert ws(batch=1, seqlen=4096, heads_q=8, heads_kv=2) == hs(1, 8, 4096, 128)
+    assert ws(batch=1, seqlen=2048, heads_q=16, heads_kv=2, head_dim=64,
+              causal=False) == hs(1, 16, 2048, 64)
+    # at the boundary: 32 steps against a share of 22.3 (1.43 x), then of
+    # 24.2 (1.32 x)
+    assert ws(batch=1, seqlen=1024, heads_q=24, heads_kv=12) == hs(1, 24, 1024, 128)
+    assert ws(batch=1, seqlen=1024, heads_q=26, heads_kv=13) == plain_bytes(1, 26, 1024)
+    # batch 4 MQA: 2048 steps against 1820 (1.125 x)
+    assert ws(batch=4, seqlen=4096, heads_q=32, heads_kv=1) == plain_bytes(4, 32, 4096)
+    # batch 8 MQA, P4, and a merged job of fewer than 32 steps: one dKV job
+    # per KV head
+    assert ws(batch=8, seqlen=4096, heads_q=32, heads_kv=1) == plain_bytes(8, 32, 4096)
+    assert ws(batch=2, seqlen=4096, heads_q=32, heads_kv=8) == plain_bytes(2, 32, 4096)
+    assert ws(batch=1, seqlen=384, heads_q=4, heads_kv=2) == plain_bytes(1, 4, 384)
+
+
 def test_legacy_workspace_sizes(lib):
     """The legacy entry sizes like v2 in either aux mode."""
     def ws(mode, **kw):

@@ -46,6 +46,9 @@ CASES = [
     (1, 2, 2, 4096, 64, True),    # M = 32, D = 64
     (1, 8, 8, 2048, 64, True),    # 512 jobs: the largest split plan
     (1, 9, 9, 2048, 64, True),    # 576 jobs: causal, one head per group, default plan
+    (1, 4, 2, 1024, 128, True),   # head-split plan: G = 2
+    (1, 8, 1, 1024, 128, True),   # head-split plan: MQA, G = 8
+    (1, 16, 2, 2048, 64, False),  # head-split plan: full attention, D = 64, persistent
 ]
 
 
@@ -67,6 +70,7 @@ def test_v2_matches_oracle(B, Hq, Hkv, S, D, causal):
     (1, 1, 1, 256, 128, True, 1.0),    # split plan (unscaled at every scale)
     (1, 1, 1, 128, 128, True, 1.0),    # level-order default plan (causal, G = 1), unscaled
     (1, 9, 9, 2048, 64, True, 1.0),    # ... persistent (576 jobs), unscaled
+    (1, 8, 1, 1024, 128, True, 1.0),   # head-split plan, unscaled
 ])
 def test_v2_softmax_scales(B, Hq, Hkv, S, D, causal, scale):
     """The default plan's score waves multiply their resident operand (K, or
@@ -101,7 +105,8 @@ def test_v2_gqa_reference_gate_shape():
     check(res, g, reference_gates=True)
 
 
-@pytest.mark.parametrize("hq,hkv,s,d", [(4, 2, 1024, 128),   # one launch plan per job
+@pytest.mark.parametrize("hq,hkv,s,d", [(4, 2, 384, 128),    # one dKV job per KV head
+                                          (8, 1, 1024, 128),   # head split: ordered reduction
                                           (2, 2, 1024, 128),   # split plan (causal, G = 1)
                                           (2, 2, 512, 64)])
 def test_deterministic_mode_is_bitwise_repeatable(hq, hkv, s, d):
@@ -312,6 +317,7 @@ def test_dot_do_o_component(lse_mode):
 @pytest.mark.parametrize("B,Hq,Hkv,S,D,causal", [
     (2, 32, 8, 4096, 128, True),    # P4 GQA
     (2, 16, 16, 8192, 64, False),   # P5
+    (1, 32, 1, 4096, 128, True),    # MQA at batch 1: head-split plan
 ])
 def test_full_size_configs(B, Hq, Hkv, S, D, causal):
     """The whole P4 / P5 backward against the oracle (forward and backward
@@ -345,18 +351,23 @@ def check_per_group(res, g):
     log({"worst group": {k: round(v, 6) for k, v in worst.items()}})
 
 
+@pytest.mark.parametrize("hq,hkv", [
+    (16, 8),  # 1536 jobs, one dKV job per KV head
+    (8, 2),   # 1024 jobs, head-split plan (a merged dKV job, 256 steps, would
+              # outlast a CU's share of the work)
+])
 @pytest.mark.parametrize("dtype,layout,scale", [
     ("bf16", "bhsd", None),   # bf16 instantiation of the persistent plan
     ("fp16", "bshd", None),   # BSHD strides in the persistent job loop
     ("fp16", "bhsd", 1.0),    # scale 1: c = log2(e) > 1, the unscaled instantiation
 ])
-def test_persistent_plan_variants(dtype, layout, scale):
-    """The persistent default plan (at least two jobs per CU: 640 jobs at B1
-    Hq8 Hkv2 S4096 D128 causal) in the instantiations the BASELINE configs do
-    not reach -- bf16, BSHD, unscaled resident operands -- against the
-    oracle, per (batch, kv-head) group; BSHD also bit-equal to BHSD."""
-    log(f"[case] persistent plan {dtype} {layout} scale={scale} B1 Hq8 Hkv2 S4096 D128 causal")
-    g = O.golden(1, 8, 2, 4096, 128, True, scale=scale, dtype=dtype)
+def test_persistent_plan_variants(dtype, layout, scale, hq, hkv):
+    """The persistent default plan (at least two jobs per CU) at B1 S4096
+    D128 causal, GQA, in the instantiations the BASELINE configs do not reach
+    -- bf16, BSHD, unscaled resident operands -- against the oracle, per
+    (batch, kv-head) group; BSHD also bit-equal to BHSD."""
+    log(f"[case] persistent plan {dtype} {layout} scale={scale} B1 Hq{hq} Hkv{hkv} S4096 D128 causal")
+    g = O.golden(1, hq, hkv, 4096, 128, True, scale=scale, dtype=dtype)
     res = run_v2(g, torch, bshd=layout == "bshd")
     assert res["status"] == F.SUCCESS, F.status_name(res["status"])
     check_per_group(res, g)
@@ -372,6 +383,7 @@ def test_persistent_plan_variants(dtype, layout, scale):
     (1, 4, 2, 256, 128, True),    # GQA
     (2, 8, 2, 256, 128, False),
     (1, 2, 2, 512, 64, True),
+    (1, 8, 1, 1024, 128, True),   # head-split plan
 ])
 def test_v2_bf16(B, Hq, Hkv, S, D, causal):
     """bf16 tensors (this build's extension): bf16 oracle, bf16 bar."""
@@ -388,6 +400,7 @@ def test_v2_bf16(B, Hq, Hkv, S, D, causal):
     (2, 8, 2, 256, 128, False, "fp16"),   # GQA, batch 2
     (1, 4, 2, 384, 64, True, "fp16"),
     (2, 4, 2, 256, 128, True, "bf16"),
+    (1, 8, 2, 1024, 64, True, "bf16"),    # head-split plan: the reduction's BSHD strides
 ])
 def test_v2_bshd(B, Hq, Hkv, S, D, causal, dtype):
     """[B, S, H, D] tensors (this build's extension), same values as BHSD:

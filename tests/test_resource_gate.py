@@ -30,13 +30,15 @@ def test_shipped_kernels_present(gated):
     for want in EXPECTED:
         assert any(want in n for n in names), want
     # every (head dim, causal, bf16) instantiation of the main kernel with
-    # scaled and unscaled resident operands (the causal ones also in the
-    # level-by-level job order), and the split-plan instantiations of the
-    # causal ones (unscaled only), without and with the code for short jobs
-    # after pieces: 32, each with its race-check twin
-    # (shaobo_fa3_ext_set_race_check), which the gate holds to the same
-    # budget
-    assert sum("bwd_main_kernel" in n for n in names) == 64
+    # scaled and unscaled resident operands, in the role-major and the
+    # head-split job orders (the causal ones also level by level), and the
+    # split-plan instantiations of the causal ones (unscaled only), without
+    # and with the code for short jobs after pieces: 48, each with its
+    # race-check twin (shaobo_fa3_ext_set_race_check), which the gate holds
+    # to the same budget
+    assert sum("bwd_main_kernel" in n for n in names) == 96
+    # the head-split plan's reduction of the per-query-head dK / dV
+    assert sum("gqa_reduce_kernel" in n for n in names) == 4
 
 
 def test_main_kernel_two_waves_per_simd(gated):

@@ -72,3 +72,33 @@ def test_no_alloc_refuses_oversized_shapes():
     # a shape that fits is accepted by the size check (sizes only)
     p = _params(lib, 2, 32, 8, 4096, 128, True, 1 / math.sqrt(128))
     assert lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p)) <= F.NO_ALLOC_SCRATCH_BYTES
+
+
+@pytest.mark.gpu
+def test_no_alloc_head_split_shapes():
+    """GQA shapes under the head-split plan: where its per-query-head dK / dV
+    fit the scratch array the entry runs that plan (bit-equal to v2); where
+    they do not (16 query heads at S4096 D128: 64 MiB), it runs the plan with
+    one dKV job per KV head instead of refusing, and meets the oracle bar."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from gpu_util import check
+    lib = F.load()
+    shape = (1, 8, 1, 1024, 128, True)
+    log(f"[case] no-alloc head split {shape}")
+    g = O.golden(*shape)
+    ref = run_v2(g, torch)
+    assert ref["status"] == F.SUCCESS
+    st, res = _run_no_alloc(g)
+    assert st == F.SUCCESS, F.status_name(st)
+    for n in ("dq", "dk", "dv", "delta"):
+        np.testing.assert_array_equal(res[n], ref[n], err_msg=n)
+    shape = (1, 16, 1, 4096, 128, True)
+    log(f"[case] no-alloc head split over the scratch size {shape}")
+    p = _params(lib, 1, 16, 1, 4096, 128, True, 1 / math.sqrt(128))
+    assert lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p)) > F.NO_ALLOC_SCRATCH_BYTES
+    g = O.golden(*shape)
+    st, res = _run_no_alloc(g)
+    assert st == F.SUCCESS, F.status_name(st)
+    res["status"] = st
+    check(res, g)
