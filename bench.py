@@ -53,6 +53,17 @@ CONFIGS = {
 }
 
 
+def register_shape(text):
+    """A --shape "B,Hq,Hkv,S,D,causal|full" as a CONFIGS entry; returns its name."""
+    parts = text.split(",")
+    if len(parts) != 6 or parts[5] not in ("causal", "full"):
+        raise SystemExit(f"--shape wants B,Hq,Hkv,S,D,causal|full, got {text!r}")
+    B, Hq, Hkv, S, D = (int(x) for x in parts[:5])
+    name = f"shape_{B}_{Hq}_{Hkv}_{S}_{D}_{parts[5]}"
+    CONFIGS[name] = (B, Hq, Hkv, S, D, parts[5] == "causal")
+    return name
+
+
 def flops(B, Hq, S, D, causal):
     return 10.0 * B * Hq * S * S * D * (0.5 if causal else 1.0)
 
@@ -393,6 +404,9 @@ def main():
                     help="untimed warm-up steps (default 20); warm-up also lasts at least "
                          "0.3 s of GPU work, which brings the clocks to their steady state")
     ap.add_argument("--config", default="P3", choices=sorted(CONFIGS))
+    ap.add_argument("--shape", default=None, metavar="B,Hq,Hkv,S,D,causal|full",
+                    help="time this shape instead of a BASELINE config (a diagnostic line, "
+                         "not the headline)")
     ap.add_argument("--all", action="store_true",
                     help="every config P1-P5, one JSON line each (GPU and whole-config CPU)")
     ap.add_argument("--deterministic", action="store_true")
@@ -418,7 +432,10 @@ def main():
         run_all(torch, lib, F, hip, args)
         return
     warmup = 20 if args.warmup is None else args.warmup
-    result = measure(torch, lib, F, hip, args.config, args.steps, warmup, args.deterministic)
+    name = args.config
+    if args.shape is not None:
+        name = register_shape(args.shape)
+    result = measure(torch, lib, F, hip, name, args.steps, warmup, args.deterministic)
     if args.calib_copy_mb > 0:
         # plain copy kernel of known size, for scaling rocprofv3 FETCH/WRITE_SIZE
         n = args.calib_copy_mb * (1 << 20) // 4
@@ -429,7 +446,7 @@ def main():
         torch.cuda.synchronize()
         result["calib_copy_bytes"] = n * 4
     if args.cpu_budget > 0:
-        result["cpu_baseline"] = cpu_baseline(CONFIGS[args.config], args.cpu_budget)
+        result["cpu_baseline"] = cpu_baseline(CONFIGS[name], args.cpu_budget)
     print(json.dumps(result), flush=True)
 
 

@@ -208,7 +208,7 @@ int run_backward(const void* dout, const void* q, const void* k, const void* v, 
     if (opt.no_alloc) {
         // the head-split plan's per-query-head dK / dV need not fit the
         // scratch array: then the plan with one dKV job per KV head
-        if (plan.ok && plan.head_split && plan.total > fa3::kNoAllocScratchBytes) {
+        if (plan.ok && plan.hs_chunks > 0 && plan.total > fa3::kNoAllocScratchBytes) {
             pr.no_head_split = true;
             plan = fa3::plan_workspace(pr);
         }

@@ -130,8 +130,8 @@ struct WorkspacePlan {
     size_t sync_off = 0;
     size_t pkv_off = 0;     // dKV pieces' partial sums
     size_t pq_off = 0;      // dQ pieces' partial sums
-    bool head_split = false;  // head-split default plan (GQA, few groups)
-    size_t hsd_off = 0;       // its fp32 dK contributions [B][Hq][S][D], then dV's
+    int hs_chunks = 0;        // > 0: head-split default plan (GQA, few groups)
+    size_t hsd_off = 0;       // its fp32 dK contributions [B][Hkv hs_chunks][S][D], then dV's
     size_t total = 0;
     bool ok = false;        // false: the sizes overflow size_t / the kernel's offsets
 };

@@ -180,18 +180,47 @@ hipError_t split_giveup_count(int dev, unsigned long long** ptr) {
     return e;
 }
 
-// The CU count the head-split decision assumes (an MI355X's): the plan, and
-// so the workspace size, depends on the shape only.
+// Head-split plan choice.  Work in dKV steps (a dQ step ~0.75 of one); a
+// CU's share = all steps / kHeadSplitCus (an MI355X's CU count: the plan,
+// and so the workspace size, depends on the shape only).  The merged plan
+// takes max(share, G QT) -- its longest job, G heads' query tiles against
+// key tile 0 -- and chunks of G / f heads take max(share, G QT / f), times
+// 1 + kHeadSplitPerChunk f (the fp32 contributions' traffic and the extra
+// prologues), plus kHeadSplitFixed for the reduction launch.  The plan picks
+// the f with the least estimate, if it is below kHeadSplitGain x the merged
+// plan's: near the boundary the estimate's error exceeds the gain (B2 Hq16
+// Hkv4 S2048 D128 causal: estimated -3 %, measured +9 %).  Measured (D 128
+// causal): 32 chunks at B1 Hq32 Hkv1 S4096 run each step of the share ~12 %
+// slower than the merged plan runs a full machine's; 8 chunks there take
+// the backward from 1 596 to 532 us, 2 chunks at B4 from 2 099 to 1 982.
 constexpr int kHeadSplitCus = 256;
-// The head-split plan runs each step of a CU's share ~10 % slower (the
-// per-head fp32 dK / dV and their reduction), and a long merged job runs
-// ~10-20 % faster than the average step once few others share its CU: it
-// pays from a merged job 1.4 x the share (B4 Hq32 Hkv1 S4096 D128 causal,
-// 1.125 x: +6.5 %; B1 Hq8 Hkv2, 2.25 x: -37 %).
-constexpr double kHeadSplitMargin = 1.4;
-// ... and the shortest merged dKV job it splits: below this, the saving is
-// less than the reduction kernel's launch.
-constexpr int kHeadSplitMinSteps = 32;
+constexpr double kHeadSplitPerChunk = 0.004;
+constexpr double kHeadSplitFixed = 8.0;
+constexpr double kHeadSplitGain = 0.92;
+
+// The chunk count f (a divisor of G, >= 2) of the head-split plan for this
+// shape, or 0 for the merged plan.  (G QT > share needs QT + 1 < 2 x 256 /
+// (1.75 B Hkv) causal, QT < 256 / (1.75 B Hkv) full: the plan never meets a
+// sequence long enough to strain the reduction's 32-bit indices.)
+int head_split_chunks(const BwdProblem& p, int qt) {
+    const int group = p.heads_kv > 0 ? p.heads_q / p.heads_kv : 0;
+    if (group < 2 || qt <= 0 || p.out_f32 || p.no_head_split) return 0;
+    const double steps = p.causal ? 0.5 * qt * (qt + 1.0) : (double)qt * qt;
+    const double share = (double)p.batch * p.heads_q * steps * 1.75 / kHeadSplitCus;
+    const double merged = std::max(share, (double)group * qt);
+    int best = 0;
+    double best_t = kHeadSplitGain * merged;
+    for (int f = 2; f <= group; ++f) {
+        if (group % f != 0) continue;
+        const double t = std::max(share, (double)(group / f) * qt) * (1.0 + kHeadSplitPerChunk * f) +
+                         kHeadSplitFixed;
+        if (t < best_t) {
+            best_t = t;
+            best = f;
+        }
+    }
+    return best;
+}
 
 WorkspacePlan plan_workspace(const BwdProblem& p) {
     WorkspacePlan w;
@@ -227,16 +256,19 @@ WorkspacePlan plan_workspace(const BwdProblem& p) {
     // Head-split default plan for GQA: when one dKV job (G heads' query
     // tiles against one key tile) is much longer than a CU's share of the
     // work, it alone sets the kernel's length (MQA at batch 1), so each dKV
-    // job runs for one query head and the G fp32 contributions are summed
-    // afterwards.  Work in dKV steps, a dQ step ~0.75 of one.
-    const int group = p.heads_kv > 0 ? p.heads_q / p.heads_kv : 0;
-    if (w.bal_m == 0 && group > 1 && qt > 0 && !p.out_f32 && !p.no_head_split) {
-        const double steps = p.causal ? 0.5 * qt * (qt + 1.0) : (double)qt * qt;
-        const double share = (double)p.batch * p.heads_q * steps * 1.75 / kHeadSplitCus;
-        if ((double)group * qt > kHeadSplitMargin * share && group * qt >= kHeadSplitMinSteps) {
-            w.head_split = true;
+    // job runs for a chunk of the heads and the chunks' fp32 contributions
+    // are summed afterwards.
+    if (w.bal_m == 0) {
+        w.hs_chunks = head_split_chunks(p, qt);
+        if (w.hs_chunks > 0) {
             w.hsd_off = at.v;
-            at = at.add(rows.mul((size_t)p.head_dim * sizeof(float) * 2).v).align();
+            const Checked parts = Checked{(size_t)p.batch}
+                                      .mul((size_t)p.heads_kv)
+                                      .mul((size_t)w.hs_chunks)
+                                      .mul((size_t)p.seqlen)
+                                      .mul((size_t)p.head_dim);
+            at = at.add(parts.mul(sizeof(float) * 2).v).align();
+            if (!parts.ok) return w;
         }
     }
     if (!at.ok || !rows.ok || rows.v > (size_t)INT32_MAX) return w;
@@ -302,10 +334,13 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     const int group = p.heads_q / p.heads_kv;
     // head split: G dKV jobs (one per query head) and G dQ jobs per key
     // tile / query tile
-    a.jobs_per_group = (p.seqlen / kTileN) * (plan.head_split ? 2 * group : 1 + group);
-    if (plan.head_split) {
+    a.jobs_per_group = (p.seqlen / kTileN) * ((plan.hs_chunks > 0 ? plan.hs_chunks : 1) + group);
+    if (plan.hs_chunks > 0) {
         a.part_dk = reinterpret_cast<float*>(ws + plan.hsd_off);
-        a.part_dv = a.part_dk + (size_t)p.batch * p.heads_q * p.seqlen * p.head_dim;
+        a.part_dv = a.part_dk + (size_t)p.batch * p.heads_kv * plan.hs_chunks * p.seqlen * p.head_dim;
+        a.hs_chunks = plan.hs_chunks;
+        a.hs_heads = group / plan.hs_chunks;
+        a.div_chunks = make_fastdiv(plan.hs_chunks);
     }
     set_job_map(a);
     a.n_jobs = a.n_groups * a.jobs_per_group;
@@ -351,14 +386,14 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     else if (p.head_dim == 128) launch_dd<128, false>(a, p.causal, p.bf16, t.stream);
     else launch_dd<64, false>(a, p.causal, p.bf16, t.stream);
     err = hipGetLastError();
-    if (err == hipSuccess && plan.head_split) {
+    if (err == hipSuccess && plan.hs_chunks > 0) {
         const dim3 rg((unsigned)((p.seqlen * (p.head_dim / 4) + 255) / 256),
                       (unsigned)(p.batch * p.heads_kv));
         _Float16* dk = static_cast<_Float16*>(t.dk);
         _Float16* dv = static_cast<_Float16*>(t.dv);
         auto reduce = [&](auto kernel) {
             hipLaunchKernelGGL(kernel, rg, dim3(256), 0, t.stream, a.part_dk, a.part_dv, dk, dv,
-                               p.heads_kv, group, p.seqlen, a.kv_rs, a.kv_hs);
+                               p.heads_kv, plan.hs_chunks, p.seqlen, a.kv_rs, a.kv_hs);
         };
         if (p.head_dim == 128) reduce(p.bf16 ? gqa_reduce_kernel<128, true> : gqa_reduce_kernel<128, false>);
         else reduce(p.bf16 ? gqa_reduce_kernel<64, true> : gqa_reduce_kernel<64, false>);

@@ -157,12 +157,16 @@ struct FusedArgs {
     float* part_q;
     uint32_t part_kv_bytes;
     uint32_t part_q_bytes;
-    // Head-split default plan (GQA with few groups): each dKV job covers one
-    // query head and writes its fp32 dK / dV contribution to
-    // part_dk / part_dv [B][Hq][S][D]; a reduce launch sums each KV head's G
-    // contributions (gqa_reduce_kernel).
+    // Head-split default plan (GQA with few groups): each dKV job covers
+    // hs_heads = G / hs_chunks query heads (chunk c: heads c hs_heads ..) and
+    // writes its fp32 dK / dV contribution to part_dk / part_dv
+    // [B][Hkv hs_chunks][S][D]; a reduce launch sums each KV head's
+    // hs_chunks contributions (gqa_reduce_kernel).
     float* part_dk;
     float* part_dv;
+    int hs_chunks;
+    int hs_heads;
+    FastDiv div_chunks;
 #ifdef FA3_TIMELINE
     unsigned long long* tl;  // per-workgroup timestamps (timeline build only, below)
 #endif
@@ -541,15 +545,15 @@ __device__ __forceinline__ int stage64_row(int j, int lane) {
     return ((lane >> 2) & 7) | ((j & 1) << 3) | (((lane >> 5) & 1) << 4) | ((j >> 1) << 5);
 }
 
-// The head-split plan's fp32 dK / dV contributions [B][Hq][S][D], as seen by
-// store_dkv (its fp32 path): one "KV head" per query head, rows of D.
+// The head-split plan's fp32 dK / dV contributions [B][Hkv chunks][S][D], as
+// seen by store_dkv (its fp32 path): one "KV head" per chunk, rows of D.
 template <int D>
 struct PartView {
     float* dk;
     float* dv;
     float scale;
     int seqlen;
-    int heads_kv;  // the query heads
+    int heads_kv;  // Hkv x chunks
     size_t kv_hs;  // seqlen * D
     static constexpr int out_f32 = 1;
     static constexpr int kv_rs = D;
@@ -850,15 +854,16 @@ __device__ __forceinline__ void debug_poison(FA3_LDS char* smem) {
 // dKV role
 // ----------------------------------------------------------------------------
 // Key tile kt of KV head hkv in batch b.  Streams query tiles [qa, qb) of
-// every query head of the group (kHeadSplit: of query head hr only, the
-// outputs being that head's fp32 contribution in part_dk / part_dv).  slot < 0:
+// every query head of the group (kHeadSplit: of the hs_heads query heads from
+// hr on, the outputs being their fp32 contribution, chunk pc of part_dk /
+// part_dv).  slot < 0:
 // the job is whole and writes dK / dV; otherwise the unit is piece slot & 1
 // of split job slot >> 1 and the pieces' partial sums meet in split_end.
 template <int D, bool kCausal, bool kBf16, int kRows = 0, bool kLateIssue = false,
           bool kScaled = true, bool kDebug = false, bool kHeadSplit = false, typename DA>
 __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b, int hkv, int kt, int qa, int qb,
                                          int slot,
-                         FA3_LDS char* smem, int tlu = 0, int hr = 0) {
+                         FA3_LDS char* smem, int tlu = 0, int hr = 0, int pc = 0) {
     static_assert(kRows == 0 || kRows == 1, "dKV rows come as -lse2/-delta or packed");
     using C = Cfg<D>;
     const int tid = opaque_tid();
@@ -871,7 +876,7 @@ __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b,
     const int QT = S / 64;
     const int group = d.group;
     const int kbase = kt * 64;
-    const int n_it = (kHeadSplit ? 1 : group) * (qb - qa);
+    const int n_it = (kHeadSplit ? d.hs_heads : group) * (qb - qa);
 
     // loader index of this wave when it loads (see Cfg::kGradLoads)
     const int ldr = C::kGradLoads ? t : w;
@@ -1201,9 +1206,9 @@ __device__ __forceinline__ void dkv_role(const FusedArgs& a, const DA& d, int b,
         // issue (into st_ld, or st_2 after a rotate) may still be landing, so
         // it stages the outputs
         if (kHeadSplit) {
-            const PartView<D> pv{a.part_dk, a.part_dv, a.scale, d.seqlen, d.heads_q,
-                                 (size_t)d.seqlen * D};
-            store_dkv<D, kBf16>(pv, b, hr, kbase, t, lane, acc, st_1);
+            const PartView<D> pv{a.part_dk, a.part_dv, a.scale, d.seqlen,
+                                 d.heads_kv * d.hs_chunks, (size_t)d.seqlen * D};
+            store_dkv<D, kBf16>(pv, b, pc, kbase, t, lane, acc, st_1);
             FA3_TL_DRAIN();
             FA3_TL(tlu, 3);
             return;
@@ -1585,9 +1590,10 @@ __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int&
 //
 // Head-split default plan (part_dk set; GQA with so few groups that one dKV
 // job, G QT steps, would outlast the average workgroup): the dKV jobs come
-// one per query head, p = G L + r for key tile L and head r, each writing
-// its head's fp32 contribution to dK / dV; gqa_reduce_kernel then sums the
-// G contributions of each KV head in head order (deterministic).
+// hs_chunks per key tile, p = hs_chunks L + c for key tile L and chunk c of
+// hs_heads query heads, each writing the chunk's fp32 contribution to dK /
+// dV; gqa_reduce_kernel then sums the hs_chunks contributions of each KV
+// head in chunk order (deterministic).
 //
 // Split plan (bal_m = M = QT / 2 > 0; causal, G = 1, few jobs): the causal
 // jobs run 1 .. QT steps, so one long job would set the kernel's length.
@@ -1761,18 +1767,18 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
         job_of(d, id, g, pos);
         // the job's level (key tile of a dKV job; a dQ job's query tile is
         // QT - 1 - level) and slot (0: dKV, r > 0: dQ of query head r - 1)
-        int level, slot, hl = 0;  // hl: the dKV job's query head within the group (kOrder 2)
+        int level, slot, hl = 0;  // hl: the dKV job's chunk of query heads (kOrder 2)
         if constexpr (kOrder == 1) {
             level = fdiv(d.div_g1, pos);
             slot = pos - level * (group + 1);
         } else {
-            // dKV jobs first: QT of them (kOrder 2: G per level, one per
-            // query head), then G dQ jobs per level
-            const int n_dkv = kOrder == 2 ? group * QT : QT;
+            // dKV jobs first: QT of them (kOrder 2: hs_chunks per level, one
+            // per chunk of query heads), then G dQ jobs per level
+            const int n_dkv = kOrder == 2 ? d.hs_chunks * QT : QT;
             if (pos < n_dkv) {
                 if constexpr (kOrder == 2) {
-                    level = fdiv(d.div_group, pos);
-                    hl = pos - level * group;
+                    level = fdiv(d.div_chunks, pos);
+                    hl = pos - level * d.hs_chunks;
                 } else {
                     level = pos;
                 }
@@ -1787,7 +1793,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
         debug_poison<D, kDebug>(smem);
         if (slot == 0) {
             dkv_role<D, kCausal, kBf16, 0, false, kScaled, kDebug, kOrder == 2>(
-                a, d, b, hkv, level, kCausal ? level : 0, QT, -1, smem, 0, hkv * group + hl);
+                a, d, b, hkv, level, kCausal ? level : 0, QT, -1, smem, 0,
+                kOrder == 2 ? hkv * group + hl * d.hs_heads : 0,
+                kOrder == 2 ? hkv * d.hs_chunks + hl : 0);
         } else {
             const int qt = QT - 1 - level;
             dq_role<D, kCausal, kBf16, 0, false, kScaled, kDebug>(
@@ -1868,24 +1876,24 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_component_kernel(FusedArgs a)
     }
 }
 
-// Head-split plan: dK / dV of KV head hkv = the sum, in query-head order,
-// of the fp32 contributions part[b][hkv G + r][:][:] of its G query heads,
-// rounded once to the outputs' type.  Block (x, bh): 1024 elements of
-// KV head bh = b Hkv + hkv, four per thread.  HBM-bound: reads G fp32
+// Head-split plan: dK / dV of KV head hkv = the sum, in chunk order, of the
+// fp32 contributions part[b][hkv chunks + c][:][:] of its chunks of query
+// heads, rounded once to the outputs' type.  Block (x, bh): 1024 elements of
+// KV head bh = b Hkv + hkv, four per thread.  HBM-bound: reads `chunks` fp32
 // values per 16-bit value written, for dK and dV.
 template <int D, bool kBf16>
 __global__ __launch_bounds__(256) void gqa_reduce_kernel(
     const float* __restrict__ part_dk, const float* __restrict__ part_dv, _Float16* __restrict__ dk,
-    _Float16* __restrict__ dv, int heads_kv, int group, int seqlen, int kv_rs, int kv_hs) {
+    _Float16* __restrict__ dv, int heads_kv, int chunks, int seqlen, int kv_rs, int kv_hs) {
     const int i = blockIdx.x * 256 + threadIdx.x;  // 4-element chunk of the head
     if (i >= seqlen * (D / 4)) return;
     const int bh = blockIdx.y;
     const int b = bh / heads_kv, hkv = bh - b * heads_kv;
     const int sq = i / (D / 4), c = i % (D / 4);
     const size_t head = (size_t)seqlen * D;
-    const size_t src = (size_t)bh * group * head + 4 * (size_t)i;
+    const size_t src = (size_t)bh * chunks * head + 4 * (size_t)i;
     f32x4 sk = *(const f32x4*)(part_dk + src), sv = *(const f32x4*)(part_dv + src);
-    for (int r = 1; r < group; ++r) {
+    for (int r = 1; r < chunks; ++r) {
         sk += *(const f32x4*)(part_dk + src + r * head);
         sv += *(const f32x4*)(part_dv + src + r * head);
     }

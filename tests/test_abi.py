@@ -223,11 +223,27 @@ def test_workspace_sizes(lib):
     assert ws(batch=1, seqlen=128, heads_q=1) == plain_bytes(1, 1, 128)
 
 
+def head_split_chunks(B, Hq, Hkv, S, causal):
+    """The head-split plan's chunk count f (0: one dKV job per KV head), by
+    the planner's estimate in dKV steps: a CU's share of all steps (256 CUs,
+    a dQ step 0.75 of a dKV step); the merged plan takes max(share, G QT),
+    f chunks of G / f heads max(share, G QT / f) x (1 + 0.004 f) + 8; the
+    least estimate wins if it is below 0.92 x the merged plan's."""
+    qt, G = S // 64, Hq // Hkv
+    steps = qt * (qt + 1) / 2 if causal else qt * qt
+    share = B * Hq * steps * 1.75 / 256
+    best, best_t = 0, 0.92 * max(share, G * qt)
+    for f in range(2, G + 1):
+        t = max(share, G // f * qt) * (1 + 0.004 * f) + 8
+        if G % f == 0 and t < best_t:
+            best, best_t = f, t
+    return best
+
+
 def test_head_split_workspace_sizes(lib):
-    """GQA shapes where one dKV job over all G query heads of a KV head (G QT
-    steps) would be over 1.4 x a CU's share of the work (256 CUs, a dQ step
-    0.75 of a dKV step) and at least 32 steps take the head-split plan: the
-    plain workspace plus fp32 dK and dV per query head (2 B Hq S D x 4
+    """GQA shapes whose merged dKV job (G QT steps: G query heads against one
+    key tile) would set the kernel's length take the head-split plan: the
+    plain workspace plus fp32 dK and dV per chunk of heads (2 B Hkv f S D x 4
     bytes).  The decision depends on the shape only."""
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
 
@@ -235,24 +251,28 @@ def test_head_split_workspace_sizes(lib):
         p = F.make_params(lib, **kw)
         return lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
 
-    def hs(B, Hq, S, D):
-        return plain_bytes(B, Hq, S) + align(2 * B * Hq * S * D * 4)
-    # MQA at batch 1: a dKV job of 32 x 64 steps against a share of 455
-    assert ws(batch=1, seqlen=4096, heads_q=32, heads_kv=1) == hs(1, 32, 4096, 128)
-    assert ws(batch=1, seqlen=4096, heads_q=8, heads_kv=2) == hs(1, 8, 4096, 128)
-    assert ws(batch=1, seqlen=2048, heads_q=16, heads_kv=2, head_dim=64,
-              causal=False) == hs(1, 16, 2048, 64)
-    # at the boundary: 32 steps against a share of 22.3 (1.43 x), then of
-    # 24.2 (1.32 x)
-    assert ws(batch=1, seqlen=1024, heads_q=24, heads_kv=12) == hs(1, 24, 1024, 128)
-    assert ws(batch=1, seqlen=1024, heads_q=26, heads_kv=13) == plain_bytes(1, 26, 1024)
-    # batch 4 MQA: 2048 steps against 1820 (1.125 x)
-    assert ws(batch=4, seqlen=4096, heads_q=32, heads_kv=1) == plain_bytes(4, 32, 4096)
-    # batch 8 MQA, P4, and a merged job of fewer than 32 steps: one dKV job
-    # per KV head
-    assert ws(batch=8, seqlen=4096, heads_q=32, heads_kv=1) == plain_bytes(8, 32, 4096)
-    assert ws(batch=2, seqlen=4096, heads_q=32, heads_kv=8) == plain_bytes(2, 32, 4096)
-    assert ws(batch=1, seqlen=384, heads_q=4, heads_kv=2) == plain_bytes(1, 4, 384)
+    def expect(B, Hq, Hkv, S, D, causal):
+        f = head_split_chunks(B, Hq, Hkv, S, causal)
+        return plain_bytes(B, Hq, S) + (align(2 * B * Hkv * f * S * D * 4) if f else 0)
+    cases = [
+        # B, Hq, Hkv, S, D, causal, chunks
+        (1, 32, 1, 4096, 128, True, 8),   # MQA at batch 1: 2048 steps against a share of 455
+        (2, 32, 1, 4096, 128, True, 4),
+        (4, 32, 1, 4096, 128, True, 2),   # 2048 against 1820
+        (8, 32, 1, 4096, 128, True, 0),   # 2048 against 3640
+        (1, 8, 2, 4096, 128, True, 4),
+        (1, 16, 2, 2048, 64, False, 4),
+        (1, 4, 2, 1024, 128, True, 2),
+        (2, 8, 2, 256, 128, False, 4),
+        (2, 16, 4, 2048, 128, True, 0),   # 128 against 115.5: under 8 % to gain
+        (2, 16, 8, 1024, 128, True, 0),
+        (2, 32, 8, 4096, 128, True, 0),   # P4
+        (1, 4, 2, 384, 128, True, 0),
+    ]
+    for B, Hq, Hkv, S, D, causal, f in cases:
+        assert head_split_chunks(B, Hq, Hkv, S, causal) == f
+        got = ws(batch=B, heads_q=Hq, heads_kv=Hkv, seqlen=S, head_dim=D, causal=causal)
+        assert got == expect(B, Hq, Hkv, S, D, causal), (B, Hq, Hkv, S, D, causal)
 
 
 def test_legacy_workspace_sizes(lib):

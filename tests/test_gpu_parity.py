@@ -46,9 +46,9 @@ CASES = [
     (1, 2, 2, 4096, 64, True),    # M = 32, D = 64
     (1, 8, 8, 2048, 64, True),    # 512 jobs: the largest split plan
     (1, 9, 9, 2048, 64, True),    # 576 jobs: causal, one head per group, default plan
-    (1, 4, 2, 1024, 128, True),   # head-split plan: G = 2
-    (1, 8, 1, 1024, 128, True),   # head-split plan: MQA, G = 8
-    (1, 16, 2, 2048, 64, False),  # head-split plan: full attention, D = 64, persistent
+    (1, 4, 2, 1024, 128, True),   # head-split plan: G = 2, one head per chunk
+    (1, 8, 1, 1024, 128, True),   # head-split plan: MQA, G = 8, one head per chunk
+    (1, 16, 2, 2048, 64, False),  # head-split plan: full, D = 64, two heads per chunk
 ]
 
 
@@ -317,7 +317,7 @@ def test_dot_do_o_component(lse_mode):
 @pytest.mark.parametrize("B,Hq,Hkv,S,D,causal", [
     (2, 32, 8, 4096, 128, True),    # P4 GQA
     (2, 16, 16, 8192, 64, False),   # P5
-    (1, 32, 1, 4096, 128, True),    # MQA at batch 1: head-split plan
+    (1, 32, 1, 4096, 128, True),    # MQA at batch 1: head-split plan, 4 heads per chunk
 ])
 def test_full_size_configs(B, Hq, Hkv, S, D, causal):
     """The whole P4 / P5 backward against the oracle (forward and backward

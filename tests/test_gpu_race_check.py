@@ -45,6 +45,7 @@ RACE_CASES = [
     (1, 9, 9, 2048, 64, True, "fp16"),     # 576 jobs: persistent plan, D 64
     (4, 16, 8, 1024, 128, True, "fp16"),   # 1536 jobs: persistent plan, GQA, D 128
     (2, 16, 4, 1024, 128, True, "fp16"),   # 1024 jobs: head-split plan
+    (1, 16, 2, 2048, 64, False, "fp16"),   # head-split plan, two query heads per chunk
     (2, 16, 4, 2048, 128, True, "fp16"),   # 1280 jobs: five per workgroup
     (2, 8, 8, 1024, 64, False, "fp16"),    # 512 jobs: persistent plan, full attention
     (1, 2, 2, 512, 128, True, "bf16"),     # bf16, split plan

@@ -78,7 +78,7 @@ def test_no_alloc_refuses_oversized_shapes():
 def test_no_alloc_head_split_shapes():
     """GQA shapes under the head-split plan: where its per-query-head dK / dV
     fit the scratch array the entry runs that plan (bit-equal to v2); where
-    they do not (16 query heads at S4096 D128: 64 MiB), it runs the plan with
+    they do not (8 chunks of 2 heads at S4096 D128: 32 MiB), it runs the plan with
     one dKV job per KV head instead of refusing, and meets the oracle bar."""
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
