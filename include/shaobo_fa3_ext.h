@@ -138,7 +138,11 @@ int shaobo_fa3_ext_bwd_v2_stages(const void* dout,
  * the library uses a static device array of SHAOBO_FA3_EXT_SCRATCH_BYTES on
  * the current GPU instead, and calls no hipMalloc / hipFree.  A shape whose
  * workspace (shaobo_fa3_bwd_v2_workspace_bytes) exceeds that size returns
- * SHAOBO_FA3_STATUS_INVALID_VALUE before any HIP call.  Inputs, outputs,
+ * SHAOBO_FA3_STATUS_INVALID_VALUE before any HIP call -- except where the
+ * excess is the head-split plan's per-chunk dK / dV (GQA with very few KV
+ * heads): then the call runs the plan with one dKV job per KV head, whose
+ * workspace is smaller, and its results meet the same bar but need not be
+ * bit-equal to v2's.  Inputs, outputs,
  * statuses and results are those of shaobo_fa3_bwd_v2_on_stream.  Every
  * call on one GPU shares that GPU's array: calls that may overlap in time on
  * one GPU (other streams, other host threads) race and must not be made. */
