@@ -197,6 +197,7 @@ constexpr int kHeadSplitCus = 256;
 constexpr double kHeadSplitPerChunk = 0.004;
 constexpr double kHeadSplitFixed = 8.0;
 constexpr double kHeadSplitGain = 0.92;
+constexpr int kHeadSplitMaxChunks = 64;
 
 // The chunk count f (a divisor of G, >= 2) of the head-split plan for this
 // shape, or 0 for the merged plan.  (G QT > share needs QT + 1 < 2 x 256 /
@@ -210,7 +211,8 @@ int head_split_chunks(const BwdProblem& p, int qt) {
     const double merged = std::max(share, (double)group * qt);
     int best = 0;
     double best_t = kHeadSplitGain * merged;
-    for (int f = 2; f <= group; ++f) {
+    // beyond 64 chunks the chunks' own cost (+26 %) outweighs any split
+    for (int f = 2; f <= std::min(group, kHeadSplitMaxChunks); ++f) {
         if (group % f != 0) continue;
         const double t = std::max(share, (double)(group / f) * qt) * (1.0 + kHeadSplitPerChunk * f) +
                          kHeadSplitFixed;

@@ -227,13 +227,13 @@ def head_split_chunks(B, Hq, Hkv, S, causal):
     """The head-split plan's chunk count f (0: one dKV job per KV head), by
     the planner's estimate in dKV steps: a CU's share of all steps (256 CUs,
     a dQ step 0.75 of a dKV step); the merged plan takes max(share, G QT),
-    f chunks of G / f heads max(share, G QT / f) x (1 + 0.004 f) + 8; the
-    least estimate wins if it is below 0.92 x the merged plan's."""
+    f chunks of G / f heads (f <= 64) max(share, G QT / f) x (1 + 0.004 f) + 8;
+    the least estimate wins if it is below 0.92 x the merged plan's."""
     qt, G = S // 64, Hq // Hkv
     steps = qt * (qt + 1) / 2 if causal else qt * qt
     share = B * Hq * steps * 1.75 / 256
     best, best_t = 0, 0.92 * max(share, G * qt)
-    for f in range(2, G + 1):
+    for f in range(2, min(G, 64) + 1):
         t = max(share, G // f * qt) * (1 + 0.004 * f) + 8
         if G % f == 0 and t < best_t:
             best, best_t = f, t
