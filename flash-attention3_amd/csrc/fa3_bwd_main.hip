@@ -16,16 +16,26 @@ namespace fa3 {
 namespace {
 
 
-// XCD-aware job map: n_groups groups of jobs_per_group jobs.
-void set_job_map(FusedArgs& a) {
+// The job count up to which an XCD's jobs run position by position across
+// its virtual groups: with a few jobs per CU, running the groups one after
+// another leaves the later groups' long jobs for the last rounds (B1 H9
+// S2048 D128 causal, 576 jobs over 9 groups: 61.4 -> 49.4 us).  With many
+// jobs per CU list scheduling evens that out, and one group at a time keeps
+// the XCD's L2 on fewer heads (interleaved at P5, 8 192 jobs: +6.5 %).
+constexpr int kInterleaveJobsPerCu = 4;
+
+// XCD-aware job map: n_groups groups of jobs_per_group jobs.  interleave:
+// see kInterleaveJobsPerCu.
+void set_job_map(FusedArgs& a, bool interleave = false) {
     int gcd8 = 8;
     while (a.n_groups % gcd8 != 0) gcd8 >>= 1;
     const int parts = 8 / gcd8;  // smallest split with n_groups * parts % 8 == 0
     const bool fits = a.jobs_per_group % parts == 0;
     a.xcd_parts = fits ? parts : 0;
-    a.part_len = fits ? a.jobs_per_group / parts : 0;
+    a.xcd_interleave = fits && interleave ? 1 : 0;
+    a.map_radix = !fits ? 0 : interleave ? a.n_groups * parts / 8 : a.jobs_per_group / parts;
     a.div_parts = make_fastdiv(a.xcd_parts);
-    a.div_part_len = make_fastdiv(a.part_len);
+    a.div_radix = make_fastdiv(a.map_radix);
     a.div_jpg = make_fastdiv(a.jobs_per_group);
 }
 
@@ -344,13 +354,14 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
         a.hs_heads = group / plan.hs_chunks;
         a.div_chunks = make_fastdiv(plan.hs_chunks);
     }
-    set_job_map(a);
+    const int cus = cu_count(t.device) & ~7;
+    set_job_map(a, (long long)a.n_groups * a.jobs_per_group <=
+                       (long long)kInterleaveJobsPerCu * std::max(cus, 8));
     a.n_jobs = a.n_groups * a.jobs_per_group;
     a.queue = queue;
     // persistent default plan once there are at least two jobs per CU: one
     // workgroup per CU (a multiple of 8, the XCD count) pulls jobs from the
     // queues, so no CU waits for the in-order dispatch of new workgroups
-    const int cus = cu_count(t.device) & ~7;
     a.persist = plan.bal_m == 0 && cus >= 8 && a.n_jobs >= 2 * cus ? cus : 0;
     a.epoch = next_epoch();
     if (epoch != nullptr) *epoch = a.epoch;

@@ -118,13 +118,17 @@ struct FusedArgs {
     // computed once on the host)
     FastDiv div_hq, div_hkv, div_group, div_g1;  // heads_q, heads_kv, group, group + 1
     // job map: n_groups (batch, kv head) groups of jobs_per_group jobs; with
-    // xcd_parts > 0 each group is split into xcd_parts interleaved parts of
-    // part_len jobs and whole parts are pinned to one XCD.
+    // xcd_parts > 0 each group is split into xcd_parts interleaved parts
+    // ("virtual groups") and whole parts are pinned to one XCD, whose id
+    // sequence runs its virtual groups one after another (xcd_interleave 0;
+    // map_radix = the part's length) or position by position across them
+    // (xcd_interleave 1; map_radix = the XCD's virtual-group count).
     int n_groups;
     int jobs_per_group;
     int xcd_parts;
-    int part_len;
-    FastDiv div_parts, div_part_len, div_jpg;  // xcd_parts, part_len, jobs_per_group
+    int map_radix;
+    int xcd_interleave;
+    FastDiv div_parts, div_radix, div_jpg;  // xcd_parts, map_radix, jobs_per_group
     // Persistent default plan (persist > 0): the grid has persist workgroups
     // (a multiple of 8, one per CU).  Job ids of the map above are dealt to
     // queues by id % 8 (the XCD the hardware would have sent them to);
@@ -1559,10 +1563,12 @@ __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int&
     if (a.xcd_parts > 0) {
         const int xcd = id & 7;
         const int n = id >> 3;
-        const int nq = fdiv(a.div_part_len, n);
-        const int v = xcd + 8 * nq;  // virtual group = (group, part)
+        const int hi = fdiv(a.div_radix, n), lo = n - hi * a.map_radix;
+        // j: the virtual group among this XCD's, k: the position in its part
+        const int j = a.xcd_interleave ? lo : hi, k = a.xcd_interleave ? hi : lo;
+        const int v = xcd + 8 * j;  // virtual group = (group, part)
         g = fdiv(a.div_parts, v);
-        pos = v - g * a.xcd_parts + a.xcd_parts * (n - nq * a.part_len);
+        pos = v - g * a.xcd_parts + a.xcd_parts * k;
     } else {
         g = fdiv(a.div_jpg, id);
         pos = id - g * a.jobs_per_group;

@@ -49,6 +49,8 @@ CASES = [
     (1, 4, 2, 1024, 128, True),   # head-split plan: G = 2, one head per chunk
     (1, 8, 1, 1024, 128, True),   # head-split plan: MQA, G = 8, one head per chunk
     (1, 16, 2, 2048, 64, False),  # head-split plan: full, D = 64, two heads per chunk
+    (1, 12, 12, 1024, 128, True), # split plan over 12 groups: XCD-interleaved job map
+    (3, 8, 2, 512, 64, False),    # 6 groups, head split, one job per workgroup, interleaved
 ]
 
 
