@@ -190,6 +190,14 @@ hipError_t split_giveup_count(int dev, unsigned long long** ptr) {
     return e;
 }
 
+// The split plan runs its workgroups in one round: past one job per CU the
+// default plan (one job per workgroup, or the persistent queues from 512
+// jobs on) measured faster for every shape tried -- 384 jobs: B1 H12 S1024
+// D128 -18 %, B1 H6 S2048 D64 -24 %; 512 jobs: B1 H8 S2048 D128 -4.8 %,
+// B1 H2 S8192 D64 -10.6 %, B1 H16 S1024 D64 +0.3 %.
+constexpr long long kSplitMaxJobs = 256;
+static_assert(kSplitMaxJobs <= kMaxSplitWgs, "one descriptor per split-plan workgroup");
+
 // Head-split plan choice.  Work in dKV steps (a dQ step ~0.75 of one); a
 // CU's share = all steps / kHeadSplitCus (an MI355X's CU count: the plan,
 // and so the workspace size, depends on the shape only).  The merged plan
@@ -248,11 +256,11 @@ WorkspacePlan plan_workspace(const BwdProblem& p) {
     at = at.add(kQueueBytes).align();
     if (!rows.ok) return w;
     // Split plan for causal shapes with one query head per KV head and few
-    // jobs (at most two per CU of an MI355X): see bwd_main_kernel.
+    // jobs (at most one per CU of an MI355X): see bwd_main_kernel.
     const int qt = p.seqlen / kTileM;
     const long long jobs = 2LL * p.batch * p.heads_q * qt;
-    if (p.causal && p.heads_q == p.heads_kv && qt >= 4 && qt % 2 == 0 && jobs <= 512) {
-        w.bal_m = qt / 2;  // <= kMaxBalM since jobs <= 512
+    if (p.causal && p.heads_q == p.heads_kv && qt >= 4 && qt % 2 == 0 && jobs <= kSplitMaxJobs) {
+        w.bal_m = qt / 2;  // <= kMaxBalM since jobs <= kSplitMaxJobs
         w.n_split = p.batch * p.heads_q * w.bal_m;
         const size_t kv_piece = (size_t)4 * 2 * (p.head_dim / 64) * 4096;
         const size_t q_piece = (size_t)4 * (p.head_dim / 64) * 4096;

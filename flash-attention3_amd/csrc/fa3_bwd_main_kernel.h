@@ -47,7 +47,7 @@
 // is the same every step (a finished stream re-loads its last tile into a
 // free stage), so every wait is a constant count.
 //
-// Split plan (causal, one query head per KV head, at most 512 jobs; see
+// Split plan (causal, one query head per KV head, at most 256 jobs; see
 // bwd_main_kernel): long jobs are cut in two pieces run by different
 // workgroups.  Each piece counts its arrival; the first to arrive stores its
 // fp32 partial sums with device-coherent stores and marks them done, the
@@ -69,7 +69,7 @@
 
 namespace fa3 {
 
-constexpr int kMaxSplitWgs = 4 * kMaxBalM;  // its workgroups: one per job
+constexpr int kMaxSplitWgs = 256;  // its workgroups: one per job, at most one per CU
 
 // Split-plan workgroup descriptor (one 32-bit word per workgroup, built on
 // the host): bits 0..1 the workgroup's kind (see bwd_main_kernel), 2..8 x,
@@ -78,8 +78,9 @@ constexpr int kMaxSplitWgs = 4 * kMaxBalM;  // its workgroups: one per job
 // unsplit), 24..31 the short dQ job (query tile < M) that the workgroup
 // runs before its piece (kind 0: between its whole dKV job and its dQ
 // remainder), kShortAfter + that tile for a short job run after the piece
-// (tiles < 127 only), or kNoShort.  The split plan has at most 512 jobs and
-// S / 64 >= 4, so M <= 128, groups <= 64 and lengths <= 256 fit.
+// (tiles < 127 only), or kNoShort.  The split plan has at most 256 jobs and
+// S / 64 >= 4, so M <= 64, groups <= 32 and lengths <= 128 fit (the fields
+// would hold 512 jobs).
 constexpr int kNoShort = 255;
 constexpr int kShortAfter = 128;
 __host__ __device__ constexpr uint32_t split_desc(int kind, int x, int g, int len, int shrt) {

@@ -10,7 +10,7 @@
 
 namespace fa3 {
 
-constexpr int kMaxBalM = 128;  // split plan: at most 512 jobs, so M = QT / 2 <= 128
+constexpr int kMaxBalM = 128;  // M = QT / 2 of a split plan (at most 256 jobs: M <= 64)
 
 // The split plan's head-piece lengths and short-job places.  Workgroup
 // times in units of one dKV step, measured on MI355X at B1 H4 S2048 D128

@@ -189,7 +189,7 @@ def plain_bytes(batch, heads_q, seqlen):
 
 def split_plan_bytes(batch, heads, seqlen, head_dim):
     """Workspace of the split plan (causal, one query head per KV head, at
-    most 512 jobs): the error word's region, lse2 and -delta rows, the
+    most 256 jobs): the error word's region, lse2 and -delta rows, the
     job-queue counters, two
     64-bit synchronisation words per split job of each role (B*H*QT/2 jobs per
     role), then the fp32 partial sums of one piece per split job -- dK/dV:
@@ -216,7 +216,9 @@ def test_workspace_sizes(lib):
     assert ws(batch=1, seqlen=2048, heads_q=4) == split_plan_bytes(1, 4, 2048, 128)
     assert ws(batch=1, seqlen=2048, heads_q=4, deterministic=True) == split_plan_bytes(1, 4, 2048, 128)
     assert ws(batch=1, seqlen=512, heads_q=2, head_dim=64) == split_plan_bytes(1, 2, 512, 64)
-    # no split: non-causal, GQA, too many jobs, or fewer than four query tiles
+    # no split: non-causal, GQA, too many jobs (512 here), or fewer than four query tiles
+    assert ws(batch=1, seqlen=2048, heads_q=8) == plain_bytes(1, 8, 2048)
+    assert ws(batch=1, seqlen=1024, heads_q=8) == split_plan_bytes(1, 8, 1024, 128)
     assert ws(batch=2, seqlen=8192, heads_q=16, head_dim=64, causal=False) == plain_bytes(2, 16, 8192)
     assert ws(batch=2, seqlen=4096, heads_q=32, heads_kv=8) == plain_bytes(2, 32, 4096)
     assert ws(batch=2, seqlen=4096, heads_q=4) == plain_bytes(2, 4, 4096)

@@ -43,13 +43,14 @@ CASES = [
     (2, 2, 2, 1024, 128, True),   # batch 2: 4 groups
     (1, 5, 5, 640, 64, True),     # M = 5, D = 64
     (1, 2, 2, 1536, 128, True),   # M = 12: short jobs after the pieces of kinds 1 and 2
-    (1, 2, 2, 4096, 64, True),    # M = 32, D = 64
-    (1, 8, 8, 2048, 64, True),    # 512 jobs: the largest split plan
+    (1, 2, 2, 4096, 64, True),    # M = 32, D = 64, 256 jobs: the largest split plan
+    (1, 8, 8, 2048, 64, True),    # 512 jobs: persistent default plan (past the split plan's 256)
     (1, 9, 9, 2048, 64, True),    # 576 jobs: causal, one head per group, default plan
     (1, 4, 2, 1024, 128, True),   # head-split plan: G = 2, one head per chunk
     (1, 8, 1, 1024, 128, True),   # head-split plan: MQA, G = 8, one head per chunk
     (1, 16, 2, 2048, 64, False),  # head-split plan: full, D = 64, two heads per chunk
-    (1, 12, 12, 1024, 128, True), # split plan over 12 groups: XCD-interleaved job map
+    (1, 12, 12, 512, 128, True),  # split plan over 12 groups: XCD-interleaved job map
+    (1, 12, 12, 1024, 128, True), # 384 jobs: one job per workgroup, interleaved
     (3, 8, 2, 512, 64, False),    # 6 groups, head split, one job per workgroup, interleaved
 ]
 
