@@ -367,10 +367,15 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
                        (long long)kInterleaveJobsPerCu * std::max(cus, 8));
     a.n_jobs = a.n_groups * a.jobs_per_group;
     a.queue = queue;
-    // persistent default plan once there are at least two jobs per CU: one
+    // persistent default plan once there are more than two jobs per CU: one
     // workgroup per CU (a multiple of 8, the XCD count) pulls jobs from the
-    // queues, so no CU waits for the in-order dispatch of new workgroups
-    a.persist = plan.bal_m == 0 && cus >= 8 && a.n_jobs >= 2 * cus ? cus : 0;
+    // queues, so no CU waits for the in-order dispatch of new workgroups.
+    // At exactly two per CU the hardware's dispatch of one job per
+    // workgroup measured faster (512 jobs: B1 H16 S1024 D128 -9.8 %, B1 H8
+    // S2048 D64 -11.2 %, B1 H16 S1024 D64 full -19.3 %, B1 H4 S4096 D128
+    // -1.1 %); from 576 jobs on the queues win (B1 H9 S2048 D128: +7.6 %
+    // without them), and below 512 too (384 jobs: +6 to +16 % with them).
+    a.persist = plan.bal_m == 0 && cus >= 8 && a.n_jobs > 2 * cus ? cus : 0;
     a.epoch = next_epoch();
     if (epoch != nullptr) *epoch = a.epoch;
     a.err = reinterpret_cast<unsigned long long*>(ws + plan.err_off);

@@ -44,7 +44,7 @@ CASES = [
     (1, 5, 5, 640, 64, True),     # M = 5, D = 64
     (1, 2, 2, 1536, 128, True),   # M = 12: short jobs after the pieces of kinds 1 and 2
     (1, 2, 2, 4096, 64, True),    # M = 32, D = 64, 256 jobs: the largest split plan
-    (1, 8, 8, 2048, 64, True),    # 512 jobs: persistent default plan (past the split plan's 256)
+    (1, 8, 8, 2048, 64, True),    # 512 jobs: one job per workgroup (past the split plan's 256)
     (1, 9, 9, 2048, 64, True),    # 576 jobs: causal, one head per group, default plan
     (1, 4, 2, 1024, 128, True),   # head-split plan: G = 2, one head per chunk
     (1, 8, 1, 1024, 128, True),   # head-split plan: MQA, G = 8, one head per chunk
@@ -365,7 +365,7 @@ def check_per_group(res, g):
     ("fp16", "bhsd", 1.0),    # scale 1: c = log2(e) > 1, the unscaled instantiation
 ])
 def test_persistent_plan_variants(dtype, layout, scale, hq, hkv):
-    """The persistent default plan (at least two jobs per CU) at B1 S4096
+    """The persistent default plan (more than two jobs per CU) at B1 S4096
     D128 causal, GQA, in the instantiations the BASELINE configs do not reach
     -- bf16, BSHD, unscaled resident operands -- against the oracle, per
     (batch, kv-head) group; BSHD also bit-equal to BHSD."""

@@ -47,7 +47,8 @@ RACE_CASES = [
     (2, 16, 4, 1024, 128, True, "fp16"),   # 1024 jobs: head-split plan
     (1, 16, 2, 2048, 64, False, "fp16"),   # head-split plan, two query heads per chunk
     (2, 16, 4, 2048, 128, True, "fp16"),   # 1280 jobs: five per workgroup
-    (2, 8, 8, 1024, 64, False, "fp16"),    # 512 jobs: persistent plan, full attention
+    (2, 8, 8, 1024, 64, False, "fp16"),    # 512 jobs: one job per workgroup, full attention
+    (3, 8, 8, 1024, 64, False, "fp16"),    # 768 jobs: persistent plan, full attention
     (1, 2, 2, 512, 128, True, "bf16"),     # bf16, split plan
 ]
 

@@ -2,7 +2,7 @@
 reference counterpart; bench.py times the main kernel alone with it):
 preprocess then main kernel equals one full call bit for bit, and repeated
 main-kernel-only launches on one workspace keep producing the full result --
-in the persistent plan (at least two jobs per CU) that needs the job queues
+in the persistent plan (more than two jobs per CU) that needs the job queues
 to reset themselves at the end of every launch, which the poisoned outputs
 between the launches would expose."""
 import ctypes
@@ -18,7 +18,8 @@ pytestmark = pytest.mark.gpu
 CASES = [
     # (B, Hq, Hkv, S, D, causal)   plan
     (1, 4, 4, 2048, 128, True),    # split plan (P3)
-    (1, 4, 4, 4096, 128, False),   # persistent: 4 heads x 64 tiles x 2 roles = 512 jobs
+    (1, 5, 5, 4096, 128, False),   # persistent: 5 heads x 64 tiles x 2 roles = 640 jobs
+    (1, 4, 4, 4096, 128, False),   # 512 jobs: one job per workgroup
     (2, 8, 2, 2048, 64, True),     # persistent, GQA, D 64 (B 2 x Hkv 2 x 32 x 5 = 640 jobs)
 ]
 

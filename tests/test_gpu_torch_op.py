@@ -136,7 +136,7 @@ def test_op_split_errors_reported_at_check():
     import shaobo_fa3_torch as T
     log("[case] torch op: split give-up reported by check_split_errors")
     lib = F.load()
-    g = O.golden(1, 2, 2, 1024, 128, True)  # split plan
+    g = O.golden(1, 4, 4, 2048, 128, True)  # split plan (P3: 64 split jobs per role)
     args = inputs(g)
     try:  # baseline: give-ups that earlier tests forced on purpose are consumed
         T.check_split_errors()
@@ -147,7 +147,7 @@ def test_op_split_errors_reported_at_check():
     raised = False
     lib.shaobo_fa3_ext_set_split_spin_limit(0)
     try:
-        for _ in range(20):
+        for _ in range(40):
             op(args, True, g["scale"])
             try:
                 T.check_split_errors()
@@ -157,7 +157,7 @@ def test_op_split_errors_reported_at_check():
                 break
     finally:
         lib.shaobo_fa3_ext_set_split_spin_limit(1 << 24)
-    assert raised, "no split wait gave up in 20 calls with spin limit 0"
+    assert raised, "no split wait gave up in 40 calls with spin limit 0"
     dq, dk, dv, delta = op(args, True, g["scale"])
     T.check_split_errors()
     res = {"dq": dq.float().cpu().numpy(), "dk": dk.float().cpu().numpy(),
