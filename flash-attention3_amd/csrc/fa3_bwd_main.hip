@@ -19,10 +19,12 @@ namespace {
 // The job count up to which an XCD's jobs run position by position across
 // its virtual groups: with a few jobs per CU, running the groups one after
 // another leaves the later groups' long jobs for the last rounds (B1 H9
-// S2048 D128 causal, 576 jobs over 9 groups: 61.4 -> 49.4 us).  With many
-// jobs per CU list scheduling evens that out, and one group at a time keeps
-// the XCD's L2 on fewer heads (interleaved at P5, 8 192 jobs: +6.5 %).
-constexpr int kInterleaveJobsPerCu = 4;
+// S2048 D128 causal, 576 jobs over 9 groups: 60.6 -> 48.0 us; B1 Hq48 Hkv12
+// S2048, 1 920 jobs: 240 -> 205 us).  With many jobs per CU list scheduling
+// evens that out, and one group at a time keeps the XCD's L2 on fewer heads
+// (interleaved at P5, 32 jobs per CU: +6.5 %; B2 H24 S2048 D64, 12 per CU:
+// +1.3 %).
+constexpr int kInterleaveJobsPerCu = 8;
 
 // XCD-aware job map: n_groups groups of jobs_per_group jobs.  interleave:
 // see kInterleaveJobsPerCu.
