@@ -16,18 +16,19 @@ namespace fa3 {
 namespace {
 
 
-// The job count up to which an XCD's jobs run position by position across
-// its virtual groups: with a few jobs per CU, running the groups one after
-// another leaves the later groups' long jobs for the last rounds (B1 H9
-// S2048 D128 causal, 576 jobs over 9 groups: 60.6 -> 48.0 us; B1 Hq48 Hkv12
-// S2048, 1 920 jobs: 240 -> 205 us).  With many jobs per CU list scheduling
-// evens that out, and one group at a time keeps the XCD's L2 on fewer heads
-// (interleaved at P5, 32 jobs per CU: +6.5 %; B2 H24 S2048 D64, 12 per CU:
-// +1.3 %).
-constexpr int kInterleaveJobsPerCu = 8;
+// An XCD's jobs run position by position across its virtual groups when the
+// longest job is at least this fraction of a CU's share of the work: run
+// group by group, the later groups' long jobs would start in the last rounds
+// and set the kernel's end (B1 H9 S2048 D128 causal: 60.6 -> 48.0 us; B1
+// Hq28 Hkv7 S4096: 524 -> 418 us).  With jobs that are short against the
+// share, list scheduling evens the end out anyway, and one group at a time
+// keeps the XCD's L2 on fewer heads (interleaved at P5, longest job 0.04 of
+// the share: +6.5 %; B1 H36 S4096 D128, 0.125: +6.9 %; B2 H24 S2048 D64,
+// 0.18: +1.3 %; B1 H19 S4096 D128, 0.24: -4.3 %).
+constexpr double kInterleaveLongest = 0.2;
 
 // XCD-aware job map: n_groups groups of jobs_per_group jobs.  interleave:
-// see kInterleaveJobsPerCu.
+// see kInterleaveLongest.
 void set_job_map(FusedArgs& a, bool interleave = false) {
     int gcd8 = 8;
     while (a.n_groups % gcd8 != 0) gcd8 >>= 1;
@@ -35,7 +36,8 @@ void set_job_map(FusedArgs& a, bool interleave = false) {
     const bool fits = a.jobs_per_group % parts == 0;
     a.xcd_parts = fits ? parts : 0;
     a.xcd_interleave = fits && interleave ? 1 : 0;
-    a.map_radix = !fits ? 0 : interleave ? a.n_groups * parts / 8 : a.jobs_per_group / parts;
+    a.xcd_vgroups = fits ? a.n_groups * parts / 8 : 0;
+    a.map_radix = !fits ? 0 : interleave ? a.xcd_vgroups : a.jobs_per_group / parts;
     a.div_parts = make_fastdiv(a.xcd_parts);
     a.div_radix = make_fastdiv(a.map_radix);
     a.div_jpg = make_fastdiv(a.jobs_per_group);
@@ -365,8 +367,15 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
         a.div_chunks = make_fastdiv(plan.hs_chunks);
     }
     const int cus = cu_count(t.device) & ~7;
-    set_job_map(a, (long long)a.n_groups * a.jobs_per_group <=
-                       (long long)kInterleaveJobsPerCu * std::max(cus, 8));
+    {
+        // the longest job (a dKV job: its G, or G / chunks, heads' query
+        // tiles) against a CU's share, in dKV steps (a dQ step ~0.75)
+        const int qt = p.seqlen / kTileN;
+        const double steps = p.causal ? 0.5 * qt * (qt + 1.0) : (double)qt * qt;
+        const double share = (double)p.batch * p.heads_q * steps * 1.75 / std::max(cus, 8);
+        const int heads = plan.hs_chunks > 0 ? group / plan.hs_chunks : group;
+        set_job_map(a, (double)heads * qt >= kInterleaveLongest * share);
+    }
     a.n_jobs = a.n_groups * a.jobs_per_group;
     a.queue = queue;
     // persistent default plan once there are more than two jobs per CU: one

@@ -120,15 +120,17 @@ struct FusedArgs {
     FastDiv div_hq, div_hkv, div_group, div_g1;  // heads_q, heads_kv, group, group + 1
     // job map: n_groups (batch, kv head) groups of jobs_per_group jobs; with
     // xcd_parts > 0 each group is split into xcd_parts interleaved parts
-    // ("virtual groups") and whole parts are pinned to one XCD, whose id
-    // sequence runs its virtual groups one after another (xcd_interleave 0;
-    // map_radix = the part's length) or position by position across them
-    // (xcd_interleave 1; map_radix = the XCD's virtual-group count).
+    // ("virtual groups"), and XCD x runs the xcd_vgroups consecutive ones
+    // from x xcd_vgroups on (so a group's parts share as few XCDs as they
+    // can), one after another (xcd_interleave 0; map_radix = the part's
+    // length) or position by position across them (xcd_interleave 1;
+    // map_radix = xcd_vgroups).
     int n_groups;
     int jobs_per_group;
     int xcd_parts;
     int map_radix;
     int xcd_interleave;
+    int xcd_vgroups;
     FastDiv div_parts, div_radix, div_jpg;  // xcd_parts, map_radix, jobs_per_group
     // Persistent default plan (persist > 0): the grid has persist workgroups
     // (a multiple of 8, one per CU).  Job ids of the map above are dealt to
@@ -1567,7 +1569,7 @@ __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int&
         const int hi = fdiv(a.div_radix, n), lo = n - hi * a.map_radix;
         // j: the virtual group among this XCD's, k: the position in its part
         const int j = a.xcd_interleave ? lo : hi, k = a.xcd_interleave ? hi : lo;
-        const int v = xcd + 8 * j;  // virtual group = (group, part)
+        const int v = xcd * a.xcd_vgroups + j;  // virtual group = (group, part)
         g = fdiv(a.div_parts, v);
         pos = v - g * a.xcd_parts + a.xcd_parts * k;
     } else {

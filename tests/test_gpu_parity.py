@@ -52,6 +52,7 @@ CASES = [
     (1, 12, 12, 512, 128, True),  # split plan over 12 groups: XCD-interleaved job map
     (1, 12, 12, 1024, 128, True), # 384 jobs: one job per workgroup, interleaved
     (3, 8, 2, 512, 64, False),    # 6 groups, head split, one job per workgroup, interleaved
+    (1, 28, 7, 1024, 128, True),  # 7 groups in 56 parts over 8 XCDs, persistent, interleaved
 ]
 
 
