@@ -356,8 +356,8 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
     a.nlse2 = nlse2;
     a.ndelta = ndelta;
     const int group = p.heads_q / p.heads_kv;
-    // head split: G dKV jobs (one per query head) and G dQ jobs per key
-    // tile / query tile
+    // per key tile / query tile: one dKV job (head split: one per chunk of
+    // G / chunks query heads) and G dQ jobs
     a.jobs_per_group = (p.seqlen / kTileN) * ((plan.hs_chunks > 0 ? plan.hs_chunks : 1) + group);
     if (plan.hs_chunks > 0) {
         a.part_dk = reinterpret_cast<float*>(ws + plan.hsd_off);
@@ -432,8 +432,10 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
             hipLaunchKernelGGL(kernel, rg, dim3(256), 0, t.stream, a.part_dk, a.part_dv, dk, dv,
                                p.heads_kv, plan.hs_chunks, p.seqlen, a.kv_rs, a.kv_hs);
         };
-        if (p.head_dim == 128) reduce(p.bf16 ? gqa_reduce_kernel<128, true> : gqa_reduce_kernel<128, false>);
-        else reduce(p.bf16 ? gqa_reduce_kernel<64, true> : gqa_reduce_kernel<64, false>);
+        if (p.head_dim == 128)
+            reduce(p.bf16 ? gqa_reduce_kernel<128, true> : gqa_reduce_kernel<128, false>);
+        else
+            reduce(p.bf16 ? gqa_reduce_kernel<64, true> : gqa_reduce_kernel<64, false>);
         err = hipGetLastError();
     }
     return err == hipSuccess ? mark(2) : err;
