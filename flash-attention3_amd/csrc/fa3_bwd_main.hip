@@ -16,27 +16,37 @@ namespace fa3 {
 namespace {
 
 
-// An XCD's jobs run position by position across its virtual groups when the
-// longest job is at least this fraction of a CU's share of the work: run
-// group by group, the later groups' long jobs would start in the last rounds
-// and set the kernel's end (B1 H9 S2048 D128 causal: 60.6 -> 48.0 us; B1
-// Hq28 Hkv7 S4096: 524 -> 418 us).  With jobs that are short against the
-// share, list scheduling evens the end out anyway, and one group at a time
-// keeps the XCD's L2 on fewer heads (interleaved at P5, longest job 0.04 of
-// the share: +6.5 %; B1 H36 S4096 D128, 0.125: +6.9 %; B2 H24 S2048 D64,
-// 0.18: +1.3 %; B1 H19 S4096 D128, 0.24: -4.3 %).
-constexpr double kInterleaveLongest = 0.2;
+// An XCD runs its K virtual groups one after another, or position by
+// position across them (longest jobs of all of them first).  Run one after
+// another, the last group's longest job starts when about share / K of a
+// CU's share of the work is left, and may set the kernel's end; one group at
+// a time keeps the XCD's L2 on fewer heads.  The map interleaves with at
+// most kInterleaveJobsPerCu jobs per CU, or when the longest job is at least
+// kInterleaveTail x share / K (all in dKV steps).  Measured: B1 H9 S2048
+// D128 causal -20.7 % (2.25 jobs per CU), B1 Hq28 Hkv7 S4096 -20.2 % (8.75,
+// longest 256 against share / K 57), B1 H19 S4096 -4.3 % (9.5; 64 against
+// 14); interleaving P4 (20 per CU; 256 against 455) left its time unchanged
+// and raised its L2 misses 1.9x, B1 H36 S4096 (18; 64 against 57) +6.9 %,
+// B2 H24 S2048 D64 (12; 32 against 29) +1.3 %, P5 (32; 128 against 896)
+// +6.5 %.
+constexpr int kInterleaveJobsPerCu = 8;
+constexpr double kInterleaveTail = 2.0;
 
-// XCD-aware job map: n_groups groups of jobs_per_group jobs.  interleave:
-// see kInterleaveLongest.
-void set_job_map(FusedArgs& a, bool interleave = false) {
+// XCD-aware job map: n_groups groups of jobs_per_group jobs.  longest:
+// the longest job, share: a CU's share of the work (both in dKV steps),
+// cus: the CU count -- for the interleave choice above (the defaults: one
+// group after another).
+void set_job_map(FusedArgs& a, double longest = 0.0, double share = 1.0, int cus = 0) {
     int gcd8 = 8;
     while (a.n_groups % gcd8 != 0) gcd8 >>= 1;
     const int parts = 8 / gcd8;  // smallest split with n_groups * parts % 8 == 0
     const bool fits = a.jobs_per_group % parts == 0;
     a.xcd_parts = fits ? parts : 0;
-    a.xcd_interleave = fits && interleave ? 1 : 0;
     a.xcd_vgroups = fits ? a.n_groups * parts / 8 : 0;
+    const long long jobs = (long long)a.n_groups * a.jobs_per_group;
+    const bool interleave = jobs <= (long long)kInterleaveJobsPerCu * cus ||
+                            longest * a.xcd_vgroups >= kInterleaveTail * share;
+    a.xcd_interleave = fits && interleave ? 1 : 0;
     a.map_radix = !fits ? 0 : interleave ? a.xcd_vgroups : a.jobs_per_group / parts;
     a.div_parts = make_fastdiv(a.xcd_parts);
     a.div_radix = make_fastdiv(a.map_radix);
@@ -374,7 +384,7 @@ hipError_t launch_backward(const BwdProblem& p, const BwdTensors& t, void* works
         const double steps = p.causal ? 0.5 * qt * (qt + 1.0) : (double)qt * qt;
         const double share = (double)p.batch * p.heads_q * steps * 1.75 / std::max(cus, 8);
         const int heads = plan.hs_chunks > 0 ? group / plan.hs_chunks : group;
-        set_job_map(a, (double)heads * qt >= kInterleaveLongest * share);
+        set_job_map(a, (double)heads * qt, share, std::max(cus, 8));
     }
     a.n_jobs = a.n_groups * a.jobs_per_group;
     a.queue = queue;
