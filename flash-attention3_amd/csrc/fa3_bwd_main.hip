@@ -46,11 +46,12 @@ void set_job_map(FusedArgs& a, double longest = 0.0, double share = 1.0, int cus
     const long long jobs = (long long)a.n_groups * a.jobs_per_group;
     const bool interleave = jobs <= (long long)kInterleaveJobsPerCu * cus ||
                             longest * a.xcd_vgroups >= kInterleaveTail * share;
-    a.xcd_interleave = fits && interleave ? 1 : 0;
+    a.xcd_interleave = interleave ? 1 : 0;
     a.map_radix = !fits ? 0 : interleave ? a.xcd_vgroups : a.jobs_per_group / parts;
     a.div_parts = make_fastdiv(a.xcd_parts);
     a.div_radix = make_fastdiv(a.map_radix);
     a.div_jpg = make_fastdiv(a.jobs_per_group);
+    a.div_groups = make_fastdiv(a.n_groups);
 }
 
 FusedArgs base_args(const BwdProblem& p, const BwdTensors& t) {

@@ -124,14 +124,16 @@ struct FusedArgs {
     // from x xcd_vgroups on (so a group's parts share as few XCDs as they
     // can), one after another (xcd_interleave 0; map_radix = the part's
     // length) or position by position across them (xcd_interleave 1;
-    // map_radix = xcd_vgroups).
+    // map_radix = xcd_vgroups).  Without parts that divide a group evenly
+    // (xcd_parts 0), ids run group by group, or position by position across
+    // all groups (xcd_interleave 1).
     int n_groups;
     int jobs_per_group;
     int xcd_parts;
     int map_radix;
     int xcd_interleave;
     int xcd_vgroups;
-    FastDiv div_parts, div_radix, div_jpg;  // xcd_parts, map_radix, jobs_per_group
+    FastDiv div_parts, div_radix, div_jpg, div_groups;  // xcd_parts, map_radix, jobs_per_group, n_groups
     // Persistent default plan (persist > 0): the grid has persist workgroups
     // (a multiple of 8, one per CU).  Job ids of the map above are dealt to
     // queues by id % 8 (the XCD the hardware would have sent them to);
@@ -1572,6 +1574,9 @@ __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int&
         const int v = xcd * a.xcd_vgroups + j;  // virtual group = (group, part)
         g = fdiv(a.div_parts, v);
         pos = v - g * a.xcd_parts + a.xcd_parts * k;
+    } else if (a.xcd_interleave) {
+        pos = fdiv(a.div_groups, id);
+        g = id - pos * a.n_groups;
     } else {
         g = fdiv(a.div_jpg, id);
         pos = id - g * a.jobs_per_group;

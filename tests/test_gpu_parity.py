@@ -53,6 +53,7 @@ CASES = [
     (1, 12, 12, 1024, 128, True), # 384 jobs: one job per workgroup, interleaved
     (3, 8, 2, 512, 64, False),    # 6 groups, head split, one job per workgroup, interleaved
     (1, 28, 7, 1024, 128, True),  # 7 groups in 56 parts over 8 XCDs, persistent, interleaved
+    (1, 7, 7, 1920, 128, True),   # 8 parts do not divide a group's 60 jobs: the map's fallback
 ]
 
 
