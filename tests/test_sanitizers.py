@@ -5,8 +5,11 @@ workspace query and entry point with random parameter structs
 under ThreadSanitizer (tests/sanitize/oracle_run.cpp), and the kernels'
 host-computed fast division against / under UBSan (tests/sanitize/fastdiv_check.cpp),
 and the split plan's planner against its invariants under ASan + UBSan
-(tests/sanitize/split_plan_check.cpp), and the stream entries' stream-device
-rule under UBSan (tests/sanitize/launch_device_check.cpp).  Built by
+(tests/sanitize/split_plan_check.cpp), the stream entries' stream-device
+rule under UBSan (tests/sanitize/launch_device_check.cpp), and the main
+kernel's job map -- a bijection onto (group, position), parts pinned to one
+XCD, longest jobs first when interleaved -- under UBSan
+(tests/sanitize/job_map_check.cpp).  Built by
 tests/sanitize/Makefile."""
 import os
 import shutil
@@ -32,7 +35,8 @@ def built():
 
 @pytest.mark.parametrize("exe,args", [("abi_asan", ["20000"]), ("oracle_asan", []),
                                       ("oracle_tsan", []), ("fastdiv_ubsan", []),
-                                      ("split_plan_asan", []), ("launch_device_ubsan", [])])
+                                      ("split_plan_asan", []), ("launch_device_ubsan", []),
+                                      ("job_map_ubsan", [])])
 def test_sanitized_run_is_clean(built, exe, args):
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1",
                UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1",
