@@ -38,7 +38,8 @@ inline void set_job_map(FusedArgs& a, double longest = 0.0, double share = 1.0, 
     a.xcd_parts = fits ? parts : 0;
     a.xcd_vgroups = fits ? a.n_groups * parts / 8 : 0;
     const long long jobs = (long long)a.n_groups * a.jobs_per_group;
-    // the groups an XCD's virtual groups belong to
+    // the groups an XCD's virtual groups belong to (one more where its
+    // first part is not a group's first)
     const int span = fits ? (a.xcd_vgroups + parts - 1) / parts : a.n_groups;
     const bool interleave =
         jobs <= (long long)kInterleaveJobsPerCu * cus ||
