@@ -221,14 +221,24 @@ def cpu_baseline(cfg, budget_s):
             "single_thread_bwd": single}
 
 
-def measure(torch, lib, F, hip, name, steps, warmup, deterministic):
+def measure(torch, lib, F, hip, name, steps, warmup, deterministic, dtype="fp16",
+            layout="bhsd"):
     """GPU figures of one config: the timed backward calls, the per-kernel
-    durations back to back, and the rooflines (no CPU baseline)."""
+    durations back to back, and the rooflines (no CPU baseline).  dtype /
+    layout: the same inputs as bf16 and / or [B, S, H, D] tensors."""
     B, Hq, Hkv, S, D, causal = CONFIGS[name]
     scale = 1.0 / math.sqrt(D)
     q, k, v, do, out, lse = make_inputs(torch, B, Hq, Hkv, S, D, causal, scale)
+    if dtype == "bf16":
+        q, k, v, do, out = (x.to(torch.bfloat16) for x in (q, k, v, do, out))
+    if layout == "bshd":
+        q, k, v, do, out = (x.transpose(1, 2).contiguous() for x in (q, k, v, do, out))
     p = F.make_params(lib, batch=B, seqlen=S, heads_q=Hq, heads_kv=Hkv, head_dim=D,
                       causal=causal, softmax_scale=scale, deterministic=deterministic)
+    if dtype == "bf16":
+        p.dtype = F.DTYPE_BF16
+    if layout == "bshd":
+        p.layout = F.LAYOUT_BSHD
     nbytes = lib.shaobo_fa3_bwd_v2_workspace_bytes(ctypes.byref(p))
     ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
@@ -288,27 +298,30 @@ def measure(torch, lib, F, hip, name, steps, warmup, deterministic):
     main_ms = hip.elapsed_ms(e0, e1) / steps
     pre_step_ms = ms - main_ms
     # the preprocess alone: the dot_do_o component runs the same kernel on
-    # the same rows (delta plus the packed sidecar: the same bytes)
-    pp = F.make_params(lib, batch=B, seqlen=S, heads_q=Hq, heads_kv=Hq, head_dim=D,
-                       causal=causal, softmax_scale=scale)
-    pp.softmax_aux_mode = F.AUX_LSE
-    packed = torch.empty(B * Hq * S * 3, dtype=torch.float32, device="cuda")
+    # the same rows (delta plus the packed sidecar: the same bytes); the
+    # component takes fp16 BHSD only, as the reference's does
+    pre_alone_ms = None
+    if dtype == "fp16" and layout == "bhsd":
+        pp = F.make_params(lib, batch=B, seqlen=S, heads_q=Hq, heads_kv=Hq, head_dim=D,
+                           causal=causal, softmax_scale=scale)
+        pp.softmax_aux_mode = F.AUX_LSE
+        packed = torch.empty(B * Hq * S * 3, dtype=torch.float32, device="cuda")
 
-    def pre_step():
-        st = lib.shaobo_fa3_bwd_dot_do_o(c(do), c(out), c(lse), None, c(delta), c(packed),
-                                         ctypes.byref(pp))
-        if st != F.SUCCESS:
-            raise RuntimeError("shaobo_fa3_bwd_dot_do_o: " + F.status_name(st))
+        def pre_step():
+            st = lib.shaobo_fa3_bwd_dot_do_o(c(do), c(out), c(lse), None, c(delta), c(packed),
+                                             ctypes.byref(pp))
+            if st != F.SUCCESS:
+                raise RuntimeError("shaobo_fa3_bwd_dot_do_o: " + F.status_name(st))
 
-    for _ in range(20):
-        pre_step()
-    torch.cuda.synchronize()
-    hip.record(e0)
-    for _ in range(steps):
-        pre_step()
-    hip.record(e1)
-    torch.cuda.synchronize()
-    pre_alone_ms = hip.elapsed_ms(e0, e1) / steps
+        for _ in range(20):
+            pre_step()
+        torch.cuda.synchronize()
+        hip.record(e0)
+        for _ in range(steps):
+            pre_step()
+        hip.record(e1)
+        torch.cuda.synchronize()
+        pre_alone_ms = hip.elapsed_ms(e0, e1) / steps
     # the same number of calls through the timed entry, three events per
     # call, read after one sync (marker-inclusive durations)
     evs = [[hip.event() for _ in range(3)] for _ in range(steps)]
@@ -334,12 +347,12 @@ def measure(torch, lib, F, hip, name, steps, warmup, deterministic):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
+        "dtype": dtype,
         "data": "synthetic",
         "config": {"workload": f"fa3_bwd_v2 {name} B{B} Hq{Hq} Hkv{Hkv} S{S} D{D} "
                                f"{'causal' if causal else 'full'}",
                    "batch": B, "heads_q": Hq, "heads_kv": Hkv, "seq_len": S, "head_dim": D,
-                   "causal": causal, "deterministic": deterministic,
+                   "causal": causal, "deterministic": deterministic, "layout": layout,
                    "flops_per_bwd": f},
         "pct_fp16_peak": round(100.0 * tflops / FP16_PEAK_TFLOPS, 3),
         "wall_s_timed": round(wall, 4),
@@ -347,7 +360,8 @@ def measure(torch, lib, F, hip, name, steps, warmup, deterministic):
         "warmup_s": round(warm_s, 3),
         "kernels_ms": {"preprocess_kernel": round(pre_step_ms, 5),
                        "bwd_main_kernel": round(main_ms, 5),
-                       "preprocess_alone_back_to_back": round(pre_alone_ms, 5)},
+                       "preprocess_alone_back_to_back":
+                           None if pre_alone_ms is None else round(pre_alone_ms, 5)},
         "kernels_ms_marked": {"preprocess_kernel": round(pre_marked, 5),
                               "bwd_main_kernel": round(main_marked, 5),
                               "ms_per_step": round(staged_ms, 5)},
@@ -407,6 +421,10 @@ def main():
     ap.add_argument("--shape", default=None, metavar="B,Hq,Hkv,S,D,causal|full",
                     help="time this shape instead of a BASELINE config (a diagnostic line, "
                          "not the headline)")
+    ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"],
+                    help="the inputs' 16-bit type (a diagnostic line; the headline is fp16)")
+    ap.add_argument("--layout", default="bhsd", choices=["bhsd", "bshd"],
+                    help="tensor layout (a diagnostic line; the headline is BHSD)")
     ap.add_argument("--all", action="store_true",
                     help="every config P1-P5, one JSON line each (GPU and whole-config CPU)")
     ap.add_argument("--deterministic", action="store_true")
@@ -435,7 +453,8 @@ def main():
     name = args.config
     if args.shape is not None:
         name = register_shape(args.shape)
-    result = measure(torch, lib, F, hip, name, args.steps, warmup, args.deterministic)
+    result = measure(torch, lib, F, hip, name, args.steps, warmup, args.deterministic,
+                     args.dtype, args.layout)
     if args.calib_copy_mb > 0:
         # plain copy kernel of known size, for scaling rocprofv3 FETCH/WRITE_SIZE
         n = args.calib_copy_mb * (1 << 20) // 4
