@@ -1777,6 +1777,14 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
     }
     // d: the argument segment, for the job's set-up (divisors); the roles
     // read the rest from a
+    // timeline build: the unit slot of the workgroup's job (the first three
+    // jobs, then the latest one in slot 3); the product build stamps nothing
+#ifdef FA3_TIMELINE
+    int tl_job = 0;
+#define FA3_TL_JOB (tl_job < 3 ? tl_job : 3)
+#else
+#define FA3_TL_JOB 0
+#endif
     auto run = [&](KArgs& d, int id) {
         job_of(d, id, g, pos);
         // the job's level (key tile of a dKV job; a dQ job's query tile is
@@ -1807,15 +1815,17 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
         debug_poison<D, kDebug>(smem);
         if (slot == 0) {
             dkv_role<D, kCausal, kBf16, 0, false, kScaled, kDebug, kOrder == 2>(
-                a, d, b, hkv, level, kCausal ? level : 0, QT, -1, smem, 0,
+                a, d, b, hkv, level, kCausal ? level : 0, QT, -1, smem, FA3_TL_JOB,
                 kOrder == 2 ? hkv * group + hl * d.hs_heads : 0,
                 kOrder == 2 ? hkv * d.hs_chunks + hl : 0);
         } else {
             const int qt = QT - 1 - level;
             dq_role<D, kCausal, kBf16, 0, false, kScaled, kDebug>(
-                a, d, b, hkv * group + slot - 1, hkv, qt, 0, kCausal ? qt + 1 : QT, -1, smem);
+                a, d, b, hkv * group + slot - 1, hkv, qt, 0, kCausal ? qt + 1 : QT, -1, smem,
+                FA3_TL_JOB);
         }
     };
+#undef FA3_TL_JOB
     // Persistent plan: thread 0 (a score wave, done with the job before the
     // gradient waves' last products and epilogue) pops the next id while
     // they finish, and passes it on through LDS; the gap's barrier
@@ -1837,6 +1847,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_main_kernel(FusedArgs a) {
         KArgs* ap = &kargs();
         __asm__ volatile("" : "+s"(ap));
         run(*ap, id);
+#ifdef FA3_TIMELINE
+        ++tl_job;
+#endif
         if (a.persist == 0) return;
         if (threadIdx.x == 0) {
             int nid = -1;

@@ -1,4 +1,4 @@
-"""Per-workgroup timeline of the main kernel (split plan: P1-P3 shapes).
+"""Per-workgroup timeline of the main kernel (BASELINE configs P1-P5).
 
 Runs one BASELINE config with the timeline build of the library
 (``make -C flash-attention3_amd timeline`` -> lib/libshaobo_fa3_bwd_timeline.so,
@@ -9,7 +9,9 @@ where each unit's time goes:
 
 Stamps (s_memrealtime, 100 MHz) per workgroup: its entry; per unit u < 4: unit
 start, resident tiles landed, loop start, last step done, unit end (stores
-complete), and for split pieces the publish / wait / add events.  Every
+complete), and for split pieces the publish / wait / add events.  A workgroup
+of the persistent plan (P4, P5) runs many jobs: its first three go to units
+0-2 and each later one overwrites unit 3, which so holds its last job.  Every
 timed launch is the main kernel alone (the stage entry) after a full call
 filled the row statistics; the instrumented kernel waits for its stores at
 each unit end, so its unit gaps and epilogues run a little long.  The timeline
@@ -125,6 +127,9 @@ def summary(cfg, rows, units, same):
                 us(U[:, S_END], U[:, S_LAST])]
         out.append(f"| {u} | {int(m.sum())} | " +
                    " | ".join(f"{np.nanmedian(x):.2f}" for x in cols) + " |")
+    if not rows[:, 29].any() and (units[:, 3, S_START] > 0).any():
+        out += ["", "Persistent plan: units 0-2 are a workgroup's first three jobs and unit 3 "
+                "its last; unit 3's first column spans the jobs between."]
     first = units[:, :, S_PUB] > 0
     second = units[:, :, S_PAST] > 0
     if first.any() or second.any():
@@ -162,7 +167,7 @@ def summary(cfg, rows, units, same):
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
-    ap.add_argument("--config", default="P3", choices=["P1", "P2", "P3"])
+    ap.add_argument("--config", default="P3", choices=["P1", "P2", "P3", "P4", "P5"])
     ap.add_argument("--raw", default=None, help="also save the raw stamps (.npy)")
     args = ap.parse_args()
     rows, units, same = record(args.config)
