@@ -133,6 +133,7 @@ struct FusedArgs {
     int map_radix;
     int xcd_interleave;
     int xcd_vgroups;
+    int xcd_mode;  // xcd_parts | xcd_interleave << 8: job_of reads both in one load
     FastDiv div_parts, div_radix, div_jpg, div_groups;  // xcd_parts, map_radix, jobs_per_group, n_groups
     // Persistent default plan (persist > 0): the grid has persist workgroups
     // (a multiple of 8, one per CU).  Job ids of the map above are dealt to
@@ -1565,16 +1566,19 @@ __device__ __forceinline__ void unit_gap() {
 // Job id -> (group, position in the group); see the job map below.
 template <typename A>
 __host__ __device__ __forceinline__ void job_of(const A& a, int id, int& g, int& pos) {
-    if (a.xcd_parts > 0) {
+    const int mode = a.xcd_mode;
+    const int parts = mode & 255;
+    const bool interleave = (mode >> 8) != 0;
+    if (parts > 0) {
         const int xcd = id & 7;
         const int n = id >> 3;
         const int hi = fdiv(a.div_radix, n), lo = n - hi * a.map_radix;
         // j: the virtual group among this XCD's, k: the position in its part
-        const int j = a.xcd_interleave ? lo : hi, k = a.xcd_interleave ? hi : lo;
+        const int j = interleave ? lo : hi, k = interleave ? hi : lo;
         const int v = xcd * a.xcd_vgroups + j;  // virtual group = (group, part)
         g = fdiv(a.div_parts, v);
-        pos = v - g * a.xcd_parts + a.xcd_parts * k;
-    } else if (a.xcd_interleave) {
+        pos = v - g * parts + parts * k;
+    } else if (interleave) {
         pos = fdiv(a.div_groups, id);
         g = id - pos * a.n_groups;
     } else {

@@ -45,6 +45,7 @@ inline void set_job_map(FusedArgs& a, double longest = 0.0, double share = 1.0, 
         jobs <= (long long)kInterleaveJobsPerCu * cus ||
         (span <= kInterleaveSpan && longest * a.xcd_vgroups >= kInterleaveTail * share);
     a.xcd_interleave = interleave ? 1 : 0;
+    a.xcd_mode = a.xcd_parts | a.xcd_interleave << 8;
     a.map_radix = !fits ? 0 : interleave ? a.xcd_vgroups : a.jobs_per_group / parts;
     a.div_parts = make_fastdiv(a.xcd_parts);
     a.div_radix = make_fastdiv(a.map_radix);
