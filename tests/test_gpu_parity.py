@@ -54,6 +54,8 @@ CASES = [
     (3, 8, 2, 512, 64, False),    # 6 groups, head split, one job per workgroup, interleaved
     (1, 28, 7, 1024, 128, True),  # 7 groups in 56 parts over 8 XCDs, persistent, interleaved
     (1, 7, 7, 1920, 128, True),   # 8 parts do not divide a group's 60 jobs: the map's fallback
+    (1, 12, 6, 1920, 128, True),  # ... GQA, persistent, fallback interleaved
+    (1, 7, 7, 1920, 64, False),   # ... full attention, D = 64
 ]
 
 
@@ -323,6 +325,7 @@ def test_dot_do_o_component(lse_mode):
     (2, 32, 8, 4096, 128, True),    # P4 GQA
     (2, 16, 16, 8192, 64, False),   # P5
     (1, 32, 1, 4096, 128, True),    # MQA at batch 1: head-split plan, 4 heads per chunk
+    (1, 19, 19, 4096, 64, True),    # 19 groups, 3 per XCD, 9.5 jobs per CU: tail interleaving
 ])
 def test_full_size_configs(B, Hq, Hkv, S, D, causal):
     """The whole P4 / P5 backward against the oracle (forward and backward
